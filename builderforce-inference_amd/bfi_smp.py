@@ -1,0 +1,261 @@
+"""ctypes binding of libbfi_sampler.so (include/bfi_sampler.h).
+
+PyTorch supplies device memory and the stream; every call goes through the C ABI to the
+HIP kernels. There is no CPU fallback: a missing library or device raises.
+Names follow the reference (crates/bfi-runtime/src/sample.rs `sample`, `target`;
+engine/spec.rs `judge` via `verify`).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbfi_sampler.so")
+
+F32, BF16 = 0, 1
+TARGET_TOKEN, TARGET_WEIGHTS = 0, 1
+
+PARAMS_DTYPE = np.dtype(
+    [
+        ("temperature", "<f4"),
+        ("top_k", "<i4"),
+        ("top_p", "<f4"),
+        ("min_p", "<f4"),
+        ("repeat_penalty", "<f4"),
+        ("presence_penalty", "<f4"),
+        ("frequency_penalty", "<f4"),
+        ("reserved", "<u4"),
+    ]
+)
+# SampleParams::default() (sample.rs:33-50), numeric fields
+DEFAULTS = dict(temperature=0.0, top_k=0, top_p=1.0, min_p=0.0, repeat_penalty=1.0,
+                presence_penalty=0.0, frequency_penalty=0.0)
+
+_lib = None
+
+
+class SamplerError(RuntimeError):
+    pass
+
+
+def lib():
+    """Loads the HIP library; raises when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise SamplerError(f"{LIB_PATH} is missing: run __graft_entry__.build() (make -C {HERE})")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.bfi_smp_create.argtypes = [I32, ctypes.POINTER(P)]
+        L.bfi_smp_destroy.argtypes = [P]
+        L.bfi_smp_destroy.restype = None
+        L.bfi_smp_last_error.argtypes = [P]
+        L.bfi_smp_last_error.restype = ctypes.c_char_p
+        L.bfi_smp_abi_version.restype = I32
+        L.bfi_smp_set_profiling.argtypes = [P, I32]
+        L.bfi_smp_profile.argtypes = [P, P, P, P]
+        L.bfi_smp_sample_rows.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P]
+        L.bfi_smp_target_rows.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P, P, P, P, P, I64, P, P]
+        L.bfi_smp_verify.argtypes = [P, P, I32, I64, I64, I64, I64, P, P, P, P, P, P, I64, P, P, P, P, P]
+        L.bfi_smp_sample_host.argtypes = [P, P, I64, P, I64, P, P, ctypes.c_float, P]
+        L.bfi_rng_next_u64.argtypes = [P]
+        L.bfi_rng_next_u64.restype = ctypes.c_uint64
+        L.bfi_rng_f32.argtypes = [P]
+        L.bfi_rng_f32.restype = ctypes.c_float
+        L.bfi_slot_rng_seed.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        L.bfi_slot_rng_seed.restype = ctypes.c_uint64
+        L.bfi_draft.argtypes = [P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, P]
+        L.bfi_draft.restype = ctypes.c_size_t
+        L.bfi_parse_id_union.argtypes = [ctypes.c_char_p, I64, P]
+        L.bfi_parse_id_union.restype = I32
+        L.bfi_spec_replay.argtypes = [P, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32, I64, ctypes.c_size_t,
+                                      ctypes.c_size_t, P, P, P, P, P, P]
+        _lib = L
+    return _lib
+
+
+def params_array(rows) -> np.ndarray:
+    if isinstance(rows, dict):
+        rows = [rows]
+    out = np.zeros(len(rows), dtype=PARAMS_DTYPE)
+    for i, r in enumerate(rows):
+        d = dict(DEFAULTS)
+        d.update(r)
+        for k, v in d.items():
+            out[i][k] = v
+    return out
+
+
+def _np_ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---- host helpers (no GPU) ---------------------------------------------------------------
+
+
+def rng_f32(state: int):
+    s = ctypes.c_uint64(state)
+    v = lib().bfi_rng_f32(ctypes.byref(s))
+    return v, s.value
+
+
+def rng_next_u64(state: int):
+    s = ctypes.c_uint64(state)
+    v = lib().bfi_rng_next_u64(ctypes.byref(s))
+    return v, s.value
+
+
+def slot_rng_seed(seed: int, prompt_len: int) -> int:
+    return lib().bfi_slot_rng_seed(seed, prompt_len)
+
+
+def draft(ctx, k, ngram_max=3, ngram_min=2):
+    c = np.ascontiguousarray(ctx, dtype=np.uint32)
+    out = np.zeros(max(k, 1), np.uint32)
+    n = lib().bfi_draft(_np_ptr(c), c.size, k, ngram_max, ngram_min, _np_ptr(out))
+    return [int(x) for x in out[:n]]
+
+
+def parse_id_union(grammar: str, n_vocab: int):
+    m = np.zeros(max((n_vocab + 31) // 32, 1), np.uint32)
+    ok = lib().bfi_parse_id_union(grammar.encode(), n_vocab, _np_ptr(m))
+    return m[: (n_vocab + 31) // 32] if ok else None
+
+
+def spec_replay(drafted, kernel_accepted, kernel_next, eos, generated, max_tokens, rng_state):
+    d = np.ascontiguousarray(drafted, dtype=np.uint32)
+    pushed = np.zeros(max(d.size, 1), np.uint32)
+    st = ctypes.c_uint64(rng_state)
+    n_pushed, acc = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    done, pend = ctypes.c_int(0), ctypes.c_int64(0)
+    rc = lib().bfi_spec_replay(_np_ptr(d), d.size, kernel_accepted, kernel_next, -1 if eos is None else eos,
+                               generated, max_tokens, ctypes.byref(st), _np_ptr(pushed), ctypes.byref(n_pushed),
+                               ctypes.byref(acc), ctypes.byref(done), ctypes.byref(pend))
+    if rc:
+        raise SamplerError("bfi_spec_replay failed")
+    return dict(pushed=[int(x) for x in pushed[: n_pushed.value]], accepted=acc.value, done=bool(done.value),
+                pending=None if pend.value < 0 else pend.value, rng_state=st.value)
+
+
+# ---- device sampler ----------------------------------------------------------------------
+
+
+def _dptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+class Sampler:
+    """One bfi_smp_ctx on a HIP device (not for concurrent use)."""
+
+    def __init__(self, device: int = 0):
+        self._L = lib()
+        self._ctx = ctypes.c_void_p()
+        rc = self._L.bfi_smp_create(device, ctypes.byref(self._ctx))
+        if rc:
+            raise SamplerError(f"bfi_smp_create: {self._L.bfi_smp_last_error(None).decode()}")
+        self.device = device
+
+    def close(self):
+        if self._ctx:
+            self._L.bfi_smp_destroy(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc:
+            raise SamplerError(f"{what} (status {rc}): {self._L.bfi_smp_last_error(self._ctx).decode()}")
+
+    @staticmethod
+    def _stream(stream):
+        if stream is None:
+            import torch
+
+            return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        return ctypes.c_void_p(stream)
+
+    def set_profiling(self, on: bool):
+        self._check(self._L.bfi_smp_set_profiling(self._ctx, 1 if on else 0), "bfi_smp_set_profiling")
+
+    def profile(self):
+        """(stream_ms, select_ms, launches) summed over the launches since the last call."""
+        a, b, n = ctypes.c_double(0), ctypes.c_double(0), ctypes.c_int64(0)
+        self._check(self._L.bfi_smp_profile(self._ctx, ctypes.byref(a), ctypes.byref(b), ctypes.byref(n)),
+                    "bfi_smp_profile")
+        return a.value, b.value, n.value
+
+    def sample_rows(self, logits, params, u, out, hist=None, hist_off=None, mask=None, stream=None):
+        """logits: cuda [B, V] float32 or bfloat16; params: cuda uint8 [B*32]; u: cuda f32 [B];
+        out: cuda int32 [B]; hist: cuda int32 ids; hist_off: cuda int64 [B+1]; mask: cuda int32 [B, W]."""
+        import torch
+
+        B, V = logits.shape
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        ms = 0 if mask is None else mask.stride(0)
+        rc = self._L.bfi_smp_sample_rows(self._ctx, _dptr(logits), dtype, B, V, logits.stride(0), _dptr(params),
+                                         _dptr(hist), _dptr(hist_off), _dptr(mask), ms, _dptr(u), _dptr(out),
+                                         self._stream(stream))
+        self._check(rc, "bfi_smp_sample_rows")
+        return out
+
+    def target_rows(self, logits, params, u, cap, hist=None, hist_off=None, mask=None, stream=None):
+        import torch
+
+        B, V = logits.shape
+        dev = logits.device
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        o = dict(
+            token=torch.zeros(B, dtype=torch.int32, device=dev),
+            kind=torch.full((B,), -1, dtype=torch.int32, device=dev),
+            kept_len=torch.zeros(B, dtype=torch.int32, device=dev),
+            listed=torch.zeros(B, dtype=torch.int32, device=dev),
+            ids=torch.zeros((B, max(cap, 1)), dtype=torch.int32, device=dev),
+            probs=torch.zeros((B, max(cap, 1)), dtype=torch.float32, device=dev),
+            stats=torch.zeros((B, 4), dtype=torch.float32, device=dev),
+        )
+        ms = 0 if mask is None else mask.stride(0)
+        rc = self._L.bfi_smp_target_rows(
+            self._ctx, _dptr(logits), dtype, B, V, logits.stride(0), _dptr(params), _dptr(hist), _dptr(hist_off),
+            _dptr(mask), ms, _dptr(u), _dptr(o["token"]), _dptr(o["kind"]), _dptr(o["kept_len"]),
+            _dptr(o["listed"]), _dptr(o["ids"]), _dptr(o["probs"]), cap, _dptr(o["stats"]), self._stream(stream))
+        self._check(rc, "bfi_smp_target_rows")
+        return o
+
+    def verify(self, logits, rows_per_seq, params, drafts, draft_len, u_pairs, u_bonus, out_accepted, out_next,
+               hist=None, hist_off=None, mask=None, stream=None):
+        """logits: cuda [n_seq*rows_per_seq, V]; params per sequence; drafts [n_seq, rows_per_seq-1]."""
+        import torch
+
+        R, V = logits.shape
+        n_seq = R // rows_per_seq
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        ms = 0 if mask is None else mask.stride(0)
+        rc = self._L.bfi_smp_verify(
+            self._ctx, _dptr(logits), dtype, n_seq, rows_per_seq, V, logits.stride(0), _dptr(params), _dptr(hist),
+            _dptr(hist_off), _dptr(drafts), _dptr(draft_len), _dptr(mask), ms, _dptr(u_pairs), _dptr(u_bonus),
+            _dptr(out_accepted), _dptr(out_next), self._stream(stream))
+        self._check(rc, "bfi_smp_verify")
+
+    def sample(self, logits, prev, params: dict, mask=None, u: float = 0.0) -> int:
+        """`sample(logits, prev, &SampleParams)` (sample.rs:304) for one host row."""
+        x = np.ascontiguousarray(logits, dtype=np.float32)
+        h = np.ascontiguousarray(prev, dtype=np.uint32)
+        p = params_array(params)
+        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
+        tok = ctypes.c_uint32(0)
+        rc = self._L.bfi_smp_sample_host(self._ctx, _np_ptr(x), x.size, _np_ptr(h), h.size, _np_ptr(p), _np_ptr(m),
+                                         u, ctypes.byref(tok))
+        self._check(rc, "bfi_smp_sample_host")
+        return tok.value
+
+    def sample_seeded(self, logits, prev, params: dict, seed: int = 0, mask=None) -> int:
+        """Exactly the reference call: u = Rng(seed).f32() (sample.rs:307)."""
+        u, _ = rng_f32(seed)
+        return self.sample(logits, prev, params, mask, u)

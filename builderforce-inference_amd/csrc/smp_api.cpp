@@ -1,0 +1,511 @@
+// smp_api.cpp — the C ABI of include/bfi_sampler.h: contexts, argument checks, device
+// workspace, launch-shape choice. No exception or abort crosses the boundary; every
+// failure is a status code plus a message (bfi_smp_last_error).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/bfi_sampler.h"
+#include "smp_device.h"
+
+#include <vector>
+
+namespace bfi {
+hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream);
+hipError_t launch_select(const KArgs& a, int bf16, hipStream_t stream);
+}
+
+struct bfi_smp_ctx {
+    int device = 0;
+    std::string err;
+    char* ws = nullptr;  // parts | cands | row_res | row_pen | row_hist
+    size_t ws_size = 0;
+    uint32_t* ctr = nullptr;  // row_ctr | seq_ctr, kept zero between launches
+    size_t ctr_words = 0;
+    bool ctr_dirty = false;
+    // staging for bfi_smp_sample_host
+    char* stage = nullptr;
+    size_t stage_size = 0;
+    // profiling: event triples around (k_stream, k_select) of each launch
+    bool profiling = false;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_used = 0;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(bfi_smp_ctx* ctx, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx)
+        ctx->err = buf;
+    else
+        g_err = buf;
+    return code;
+}
+
+int hip_fail(bfi_smp_ctx* ctx, hipError_t e, const char* what) {
+    if (ctx) ctx->ctr_dirty = true;
+    return fail(ctx, BFI_SMP_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) err = hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+int ceil_log2(int64_t v) {
+    int b = 0;
+    while ((int64_t(1) << b) < v) b++;
+    return b;
+}
+
+// Launch shape: 16-byte vectors per thread -> chunk of BLOCK*VEC*EPV elements. The largest
+// chunk that still gives >= 1024 workgroups (4 per CU on 256 CUs); at most 256 chunks/row.
+struct Shape {
+    int vec, chunk, n_chunks;
+};
+
+bool choose_shape(int64_t n_rows, int64_t V, int bf16, Shape& s) {
+    const int epv = bf16 ? 8 : 4;
+    const int vecs_f32[3] = {8, 4, 2}, vecs_bf16[3] = {4, 2, 1};
+    const int* vecs = bf16 ? vecs_bf16 : vecs_f32;
+    bool found = false;
+    for (int i = 0; i < 3; i++) {
+        int chunk = bfi::BLOCK * vecs[i] * epv;
+        int64_t nc = (V + chunk - 1) / chunk;
+        if (nc > bfi::BLOCK) continue;
+        s = Shape{vecs[i], chunk, (int)nc};
+        found = true;
+        if (n_rows * nc >= 1024) break;
+    }
+    return found;
+}
+
+struct Layout {
+    size_t parts, cands, row_res, row_pen, row_hist, total;
+};
+
+Layout layout(int64_t n_rows, const Shape& s, int bm_words) {
+    Layout L;
+    size_t off = 0;
+    L.parts = off;
+    off = align_up(off + (size_t)n_rows * s.n_chunks * sizeof(bfi::ChunkPart), 256);
+    L.cands = off;
+    off = align_up(off + (size_t)n_rows * s.n_chunks * bfi::CAND_CAP * sizeof(bfi::Cand), 256);
+    L.row_res = off;
+    off = align_up(off + (size_t)n_rows * 2 * sizeof(uint32_t), 256);
+    L.row_pen = off;
+    off = align_up(off + (size_t)n_rows * (2 * (size_t)bm_words + bfi::GDCAP) * sizeof(uint32_t), 256);
+    L.row_hist = off;
+    off = align_up(off + (size_t)n_rows * bfi::NBUCKET * 2 * sizeof(uint64_t), 256);
+    L.total = off;
+    return L;
+}
+
+int ensure_ws(bfi_smp_ctx* ctx, size_t bytes, size_t ctr_words, hipStream_t stream) {
+    if (bytes > ctx->ws_size) {
+        if (ctx->ws) (void)hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_size = 0;
+        size_t want = bytes + bytes / 4;
+        if (hipMalloc((void**)&ctx->ws, want) != hipSuccess) {
+            ctx->ws = nullptr;
+            return fail(ctx, BFI_SMP_ENOMEM, "workspace allocation of %zu bytes failed", want);
+        }
+        ctx->ws_size = want;
+    }
+    if (ctr_words > ctx->ctr_words || ctx->ctr_dirty) {
+        if (ctr_words > ctx->ctr_words) {
+            if (ctx->ctr) (void)hipFree(ctx->ctr);
+            ctx->ctr = nullptr;
+            ctx->ctr_words = 0;
+            size_t want = ctr_words < 4096 ? 4096 : ctr_words * 2;
+            if (hipMalloc((void**)&ctx->ctr, want * sizeof(uint32_t)) != hipSuccess) {
+                ctx->ctr = nullptr;
+                return fail(ctx, BFI_SMP_ENOMEM, "counter allocation failed");
+            }
+            ctx->ctr_words = want;
+        }
+        hipError_t e = hipMemsetAsync(ctx->ctr, 0, ctx->ctr_words * sizeof(uint32_t), stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipMemsetAsync(counters)");
+        ctx->ctr_dirty = false;
+    }
+    return BFI_SMP_OK;
+}
+
+struct Call {
+    const void* logits;
+    int dtype;
+    int64_t n_rows, V, row_stride;
+    const bfi_smp_row_params* params;
+    const uint32_t* hist;
+    const int64_t* hist_off;
+    const uint32_t* mask;
+    int64_t mask_stride;
+    const float* u;
+    uint32_t* out;
+    // target
+    int32_t *kind = nullptr, *kept = nullptr, *listed = nullptr;
+    uint32_t* ids = nullptr;
+    float* probs = nullptr;
+    int64_t cap = 0;
+    float* stats = nullptr;
+    // verify
+    int64_t rows_per_seq = 0, n_seq = 0;
+    const uint32_t* drafts = nullptr;
+    const int32_t* draft_len = nullptr;
+    const float *u_pairs = nullptr, *u_bonus = nullptr;
+    int32_t* out_acc = nullptr;
+    uint32_t* out_next = nullptr;
+};
+
+int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
+    if (c.dtype != BFI_SMP_F32 && c.dtype != BFI_SMP_BF16)
+        return fail(ctx, BFI_SMP_EINVAL, "dtype %d is not BFI_SMP_F32 or BFI_SMP_BF16", c.dtype);
+    if (c.n_rows < 0 || c.V < 0) return fail(ctx, BFI_SMP_EINVAL, "negative n_rows or n_vocab");
+    if (c.n_rows == 0) return BFI_SMP_OK;
+    if (c.V > (int64_t)1 << 21)
+        return fail(ctx, BFI_SMP_EINVAL, "n_vocab %lld exceeds the supported 2097152", (long long)c.V);
+    if (c.n_rows > (int64_t)1 << 24) return fail(ctx, BFI_SMP_EINVAL, "too many rows");
+    if (!c.params) return fail(ctx, BFI_SMP_EINVAL, "params is NULL");
+    if (c.V > 0 && !c.logits) return fail(ctx, BFI_SMP_EINVAL, "logits is NULL");
+    if (c.V > 0 && c.row_stride < c.V) return fail(ctx, BFI_SMP_EINVAL, "row_stride < n_vocab");
+    if (c.hist_off && !c.hist) return fail(ctx, BFI_SMP_EINVAL, "hist_off given without hist");
+    const int bm_words = (int)((c.V + 31) / 32);
+    if (c.mask && c.mask_stride < bm_words)
+        return fail(ctx, BFI_SMP_EINVAL, "mask_stride %lld < ceil(n_vocab/32) = %d", (long long)c.mask_stride, bm_words);
+    const bool verify = c.rows_per_seq > 0;
+    if (verify) {
+        if (!c.drafts && c.rows_per_seq > 1) return fail(ctx, BFI_SMP_EINVAL, "drafts is NULL");
+        if (!c.draft_len || !c.u_bonus || !c.out_acc || !c.out_next)
+            return fail(ctx, BFI_SMP_EINVAL, "verify output/input pointer is NULL");
+        if (c.rows_per_seq > 1 && !c.u_pairs) return fail(ctx, BFI_SMP_EINVAL, "u_pairs is NULL");
+    } else {
+        if (!c.u) return fail(ctx, BFI_SMP_EINVAL, "u is NULL");
+        if (!c.out) return fail(ctx, BFI_SMP_EINVAL, "out is NULL");
+        if (c.kind && (!c.kept || !c.listed || (c.cap > 0 && (!c.ids || !c.probs))))
+            return fail(ctx, BFI_SMP_EINVAL, "target outputs incomplete");
+        if (c.cap < 0) return fail(ctx, BFI_SMP_EINVAL, "cap < 0");
+    }
+    if (c.V == 0) {
+        // sample.rs:327-329: empty logits -> Token(0)
+        return fail(ctx, BFI_SMP_EINVAL, "n_vocab == 0 on the device path (use bfi_smp_sample_host)");
+    }
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+
+    Shape s;
+    if (!choose_shape(c.n_rows, c.V, c.dtype == BFI_SMP_BF16, s))
+        return fail(ctx, BFI_SMP_EINVAL, "no launch shape for n_vocab %lld", (long long)c.V);
+    const Layout L = layout(c.n_rows, s, bm_words);
+    const size_t ctr_words = (size_t)c.n_rows + (size_t)(verify ? c.n_seq : 0);
+    int rc = ensure_ws(ctx, L.total, ctr_words, stream);
+    if (rc) return rc;
+
+    bfi::KArgs a;
+    memset(&a, 0, sizeof a);
+    a.logits = c.logits;
+    a.row_stride = c.row_stride;
+    a.V = (int32_t)c.V;
+    a.n_rows = (int32_t)c.n_rows;
+    a.n_chunks = s.n_chunks;
+    a.chunk = s.chunk;
+    const size_t esz = c.dtype == BFI_SMP_BF16 ? 2 : 4;
+    a.vec_ok = ((uintptr_t)c.logits % 16 == 0) && ((size_t)c.row_stride * esz % 16 == 0);
+    a.fix_bits = 62 - ceil_log2(c.V);
+    a.params = c.params;
+    a.hist = c.hist;
+    a.hist_off = c.hist_off;
+    a.mask = c.mask;
+    a.mask_stride = c.mask_stride;
+    a.u = c.u;
+    a.out_tok = c.out;
+    a.t_kind = c.kind;
+    a.t_kept = c.kept;
+    a.t_listed = c.listed;
+    a.t_ids = c.ids;
+    a.t_probs = c.probs;
+    a.t_cap = c.cap;
+    a.t_stats = c.stats;
+    a.rows_per_seq = (int32_t)c.rows_per_seq;
+    a.drafts = c.drafts;
+    a.draft_len = c.draft_len;
+    a.u_pairs = c.u_pairs;
+    a.u_bonus = c.u_bonus;
+    a.out_accepted = c.out_acc;
+    a.out_next = c.out_next;
+    a.parts = (bfi::ChunkPart*)(ctx->ws + L.parts);
+    a.cands = (bfi::Cand*)(ctx->ws + L.cands);
+    a.row_res = (uint32_t*)(ctx->ws + L.row_res);
+    a.row_pen = (uint32_t*)(ctx->ws + L.row_pen);
+    a.row_hist = (uint64_t*)(ctx->ws + L.row_hist);
+    a.row_ctr = ctx->ctr;
+    a.seq_ctr = ctx->ctr + c.n_rows;
+    a.bm_words = bm_words;
+
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    if (ctx->profiling) {
+        if (ctx->ev_used + 3 > ctx->ev_pool.size()) {
+            if (ctx->ev_pool.size() >= 3 * 65536) return fail(ctx, BFI_SMP_EINVAL, "profiling record full: read it");
+            for (int i = 0; i < 3 * 256; i++) {
+                hipEvent_t x;
+                hipError_t ee = hipEventCreate(&x);
+                if (ee != hipSuccess) return hip_fail(ctx, ee, "hipEventCreate");
+                ctx->ev_pool.push_back(x);
+            }
+        }
+        for (int i = 0; i < 3; i++) ev[i] = ctx->ev_pool[ctx->ev_used + i];
+        ctx->ev_used += 3;
+    }
+    const int bf16 = c.dtype == BFI_SMP_BF16;
+    hipError_t e = hipSuccess;
+    if (ev[0] && (e = hipEventRecord(ev[0], stream)) != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
+    if ((e = bfi::launch_stream(a, bf16, s.vec, stream)) != hipSuccess) return hip_fail(ctx, e, "k_stream launch");
+    if (ev[1] && (e = hipEventRecord(ev[1], stream)) != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
+    if ((e = bfi::launch_select(a, bf16, stream)) != hipSuccess) return hip_fail(ctx, e, "k_select launch");
+    if (ev[2] && (e = hipEventRecord(ev[2], stream)) != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
+    return BFI_SMP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bfi_smp_abi_version(void) { return BFI_SMP_ABI_VERSION; }
+
+int bfi_smp_create(int device, bfi_smp_ctx** out) {
+    if (!out) return fail(nullptr, BFI_SMP_EINVAL, "out is NULL");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(nullptr, BFI_SMP_EHIP, "no HIP device available");
+    if (device < 0 || device >= n) return fail(nullptr, BFI_SMP_EINVAL, "device %d out of range (%d devices)", device, n);
+    bfi_smp_ctx* ctx = new (std::nothrow) bfi_smp_ctx();
+    if (!ctx) return fail(nullptr, BFI_SMP_ENOMEM, "context allocation failed");
+    ctx->device = device;
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) {
+        delete ctx;
+        return fail(nullptr, BFI_SMP_EHIP, "hipSetDevice(%d): %s", device, hipGetErrorString(g.err));
+    }
+    *out = ctx;
+    return BFI_SMP_OK;
+}
+
+void bfi_smp_destroy(bfi_smp_ctx* ctx) {
+    if (!ctx) return;
+    {
+        DeviceGuard g(ctx->device);
+        for (hipEvent_t e : ctx->ev_pool) (void)hipEventDestroy(e);
+        if (ctx->ws) (void)hipFree(ctx->ws);
+        if (ctx->ctr) (void)hipFree(ctx->ctr);
+        if (ctx->stage) (void)hipFree(ctx->stage);
+    }
+    delete ctx;
+}
+
+int bfi_smp_set_profiling(bfi_smp_ctx* ctx, int enabled) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    ctx->profiling = enabled != 0;
+    ctx->ev_used = 0;
+    return BFI_SMP_OK;
+}
+
+int bfi_smp_profile(bfi_smp_ctx* ctx, double* stream_ms, double* select_ms, int64_t* launches) {
+    if (!ctx || !stream_ms || !select_ms || !launches) return fail(ctx, BFI_SMP_EINVAL, "NULL argument");
+    DeviceGuard g(ctx->device);
+    double a = 0.0, b = 0.0;
+    const size_t n = ctx->ev_used / 3;
+    for (size_t i = 0; i < n; i++) {
+        hipEvent_t* e = &ctx->ev_pool[3 * i];
+        hipError_t r = hipEventSynchronize(e[2]);
+        if (r != hipSuccess) return hip_fail(ctx, r, "hipEventSynchronize");
+        float t1 = 0.0f, t2 = 0.0f;
+        if ((r = hipEventElapsedTime(&t1, e[0], e[1])) != hipSuccess) return hip_fail(ctx, r, "hipEventElapsedTime");
+        if ((r = hipEventElapsedTime(&t2, e[1], e[2])) != hipSuccess) return hip_fail(ctx, r, "hipEventElapsedTime");
+        a += t1;
+        b += t2;
+    }
+    *stream_ms = a;
+    *select_ms = b;
+    *launches = (int64_t)n;
+    ctx->ev_used = 0;
+    return BFI_SMP_OK;
+}
+
+const char* bfi_smp_last_error(const bfi_smp_ctx* ctx) {
+    return ctx ? ctx->err.c_str() : g_err.c_str();
+}
+
+int bfi_smp_sample_rows(bfi_smp_ctx* ctx, const void* d_logits, int dtype, int64_t n_rows, int64_t n_vocab,
+                        int64_t row_stride, const bfi_smp_row_params* d_params, const uint32_t* d_hist,
+                        const int64_t* d_hist_off, const uint32_t* d_mask, int64_t mask_stride, const float* d_u,
+                        uint32_t* d_out, void* stream) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    Call c{};
+    c.logits = d_logits;
+    c.dtype = dtype;
+    c.n_rows = n_rows;
+    c.V = n_vocab;
+    c.row_stride = row_stride;
+    c.params = d_params;
+    c.hist = d_hist;
+    c.hist_off = d_hist_off;
+    c.mask = d_mask;
+    c.mask_stride = mask_stride;
+    c.u = d_u;
+    c.out = d_out;
+    return run(ctx, c, (hipStream_t)stream);
+}
+
+int bfi_smp_target_rows(bfi_smp_ctx* ctx, const void* d_logits, int dtype, int64_t n_rows, int64_t n_vocab,
+                        int64_t row_stride, const bfi_smp_row_params* d_params, const uint32_t* d_hist,
+                        const int64_t* d_hist_off, const uint32_t* d_mask, int64_t mask_stride, const float* d_u,
+                        uint32_t* d_token, int32_t* d_kind, int32_t* d_kept_len, int32_t* d_listed,
+                        uint32_t* d_ids, float* d_probs, int64_t cap, float* d_stats, void* stream) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    if (!d_kind) return fail(ctx, BFI_SMP_EINVAL, "kind is NULL");
+    Call c{};
+    c.logits = d_logits;
+    c.dtype = dtype;
+    c.n_rows = n_rows;
+    c.V = n_vocab;
+    c.row_stride = row_stride;
+    c.params = d_params;
+    c.hist = d_hist;
+    c.hist_off = d_hist_off;
+    c.mask = d_mask;
+    c.mask_stride = mask_stride;
+    c.u = d_u;
+    c.out = d_token;
+    c.kind = d_kind;
+    c.kept = d_kept_len;
+    c.listed = d_listed;
+    c.ids = d_ids;
+    c.probs = d_probs;
+    c.cap = cap;
+    c.stats = d_stats;
+    return run(ctx, c, (hipStream_t)stream);
+}
+
+int bfi_smp_verify(bfi_smp_ctx* ctx, const void* d_logits, int dtype, int64_t n_seq, int64_t rows_per_seq,
+                   int64_t n_vocab, int64_t row_stride, const bfi_smp_row_params* d_params, const uint32_t* d_hist,
+                   const int64_t* d_hist_off, const uint32_t* d_drafts, const int32_t* d_draft_len,
+                   const uint32_t* d_mask, int64_t mask_stride, const float* d_u_pairs, const float* d_u_bonus,
+                   int32_t* d_out_accepted, uint32_t* d_out_next, void* stream) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    if (rows_per_seq < 1) return fail(ctx, BFI_SMP_EINVAL, "rows_per_seq must be >= 1");
+    if (n_seq < 0) return fail(ctx, BFI_SMP_EINVAL, "n_seq < 0");
+    Call c{};
+    c.logits = d_logits;
+    c.dtype = dtype;
+    c.n_rows = n_seq * rows_per_seq;
+    c.V = n_vocab;
+    c.row_stride = row_stride;
+    c.params = d_params;
+    c.hist = d_hist;
+    c.hist_off = d_hist_off;
+    c.mask = d_mask;
+    c.mask_stride = mask_stride;
+    c.rows_per_seq = rows_per_seq;
+    c.n_seq = n_seq;
+    c.drafts = d_drafts;
+    c.draft_len = d_draft_len;
+    c.u_pairs = d_u_pairs;
+    c.u_bonus = d_u_bonus;
+    c.out_acc = d_out_accepted;
+    c.out_next = d_out_next;
+    return run(ctx, c, (hipStream_t)stream);
+}
+
+int bfi_smp_sample_host(bfi_smp_ctx* ctx, const float* logits, int64_t n_vocab, const uint32_t* prev,
+                        int64_t n_prev, const bfi_smp_row_params* params, const uint32_t* allow_mask, float u,
+                        uint32_t* out_token) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    if (!out_token || !params) return fail(ctx, BFI_SMP_EINVAL, "out_token or params is NULL");
+    if (n_vocab < 0 || n_prev < 0) return fail(ctx, BFI_SMP_EINVAL, "negative size");
+    if (n_vocab == 0) {  // sample.rs:327-329
+        *out_token = 0;
+        return BFI_SMP_OK;
+    }
+    if (!logits) return fail(ctx, BFI_SMP_EINVAL, "logits is NULL");
+    if (n_prev > 0 && !prev) return fail(ctx, BFI_SMP_EINVAL, "prev is NULL");
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+    const int64_t mw = (n_vocab + 31) / 32;
+    size_t off = 0;
+    const size_t o_log = off;
+    off = align_up(off + (size_t)n_vocab * 4, 256);
+    const size_t o_hist = off;
+    off = align_up(off + (size_t)(n_prev ? n_prev : 1) * 4, 256);
+    const size_t o_off = off;
+    off = align_up(off + 2 * 8, 256);
+    const size_t o_mask = off;
+    off = align_up(off + (size_t)mw * 4, 256);
+    const size_t o_par = off;
+    off = align_up(off + sizeof(bfi_smp_row_params), 256);
+    const size_t o_u = off;
+    off = align_up(off + 4, 256);
+    const size_t o_out = off;
+    off = align_up(off + 4, 256);
+    if (off > ctx->stage_size) {
+        if (ctx->stage) (void)hipFree(ctx->stage);
+        ctx->stage = nullptr;
+        ctx->stage_size = 0;
+        if (hipMalloc((void**)&ctx->stage, off) != hipSuccess) {
+            ctx->stage = nullptr;
+            return fail(ctx, BFI_SMP_ENOMEM, "staging allocation failed");
+        }
+        ctx->stage_size = off;
+    }
+    char* d = ctx->stage;
+    int64_t hoff[2] = {0, n_prev};
+    hipError_t e;
+    if ((e = hipMemcpy(d + o_log, logits, (size_t)n_vocab * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+        (n_prev && (e = hipMemcpy(d + o_hist, prev, (size_t)n_prev * 4, hipMemcpyHostToDevice)) != hipSuccess) ||
+        (e = hipMemcpy(d + o_off, hoff, sizeof hoff, hipMemcpyHostToDevice)) != hipSuccess ||
+        (allow_mask && (e = hipMemcpy(d + o_mask, allow_mask, (size_t)mw * 4, hipMemcpyHostToDevice)) != hipSuccess) ||
+        (e = hipMemcpy(d + o_par, params, sizeof *params, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(d + o_u, &u, 4, hipMemcpyHostToDevice)) != hipSuccess)
+        return hip_fail(ctx, e, "hipMemcpy to device");
+    Call c{};
+    c.logits = d + o_log;
+    c.dtype = BFI_SMP_F32;
+    c.n_rows = 1;
+    c.V = n_vocab;
+    c.row_stride = n_vocab;
+    c.params = (const bfi_smp_row_params*)(d + o_par);
+    c.hist = (const uint32_t*)(d + o_hist);
+    c.hist_off = (const int64_t*)(d + o_off);
+    c.mask = allow_mask ? (const uint32_t*)(d + o_mask) : nullptr;
+    c.mask_stride = mw;
+    c.u = (const float*)(d + o_u);
+    c.out = (uint32_t*)(d + o_out);
+    int rc = run(ctx, c, nullptr);
+    if (rc) return rc;
+    if ((e = hipMemcpy(out_token, d + o_out, 4, hipMemcpyDeviceToHost)) != hipSuccess)
+        return hip_fail(ctx, e, "hipMemcpy to host");
+    return BFI_SMP_OK;
+}
+
+}  // extern "C"

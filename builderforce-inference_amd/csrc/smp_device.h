@@ -1,0 +1,329 @@
+// smp_device.h — device building blocks of the gfx950 sampler kernel.
+//
+// Wave64 reductions/scans (DPP-lowered shuffles), block (256-thread, 4-wave) reductions
+// through LDS, the order-preserving float key, and the penalty/mask transform that restates
+// crates/bfi-runtime/src/sample.rs:331-375 element by element.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/bfi_sampler.h"
+
+namespace bfi {
+
+constexpr int BLOCK = 256;  // threads per workgroup (4 wave64s)
+constexpr int WAVE = 64;
+constexpr int NWAVE = BLOCK / WAVE;
+constexpr int CHUNK_MAX = 8192;        // logits elements per workgroup (stream phase)
+constexpr int CAND_CAP = 512;          // candidates one chunk may hand to the combine
+constexpr int NMAX = 2048;             // combine sort capacity (power of two)
+constexpr int NBUCKET = 1024;          // radix buckets (10-bit digits) of the fallback select
+constexpr int DCAP = 1024;             // distinct history ids counted per chunk in LDS
+constexpr int GDCAP = 4096;            // distinct history ids counted per row (global scratch)
+constexpr uint32_t NCAND_UNBOUNDED = 0xFFFFFFFFu;  // row has no top-k / min-p bound
+constexpr uint32_t NCAND_OVERFLOW = 0xFFFFFFFEu;   // chunk had more than CAND_CAP candidates
+constexpr float F32_EPS = 1.1920928955078125e-07f;  // f32::EPSILON
+
+// Per (row, chunk) result of the stream phase.
+struct ChunkPart {
+    float m;          // max of s = penalized/T (or of penalized logits when greedy)
+    float sum;        // sum over the chunk of exp(s - m)
+    uint32_t arg;     // greedy: first index attaining m
+    uint32_t ncand;   // candidates written, or NCAND_UNBOUNDED / NCAND_OVERFLOW
+    float theta;      // every element of the chunk with finite s >= theta was written
+    float raw_m;      // max of masked, un-penalized logits (only when min_p > 1)
+    uint32_t raw_arg; // its first index
+    uint32_t pad;
+};
+
+struct Cand {
+    uint32_t idx;
+    float s;
+};
+
+// Everything a launch needs; passed by value.
+struct KArgs {
+    const void* logits;
+    int64_t row_stride;
+    int32_t V;
+    int32_t n_rows;
+    int32_t n_chunks;
+    int32_t chunk;  // elements per chunk
+    int32_t vec_ok; // rows are 16-byte aligned: vector loads allowed
+    int32_t fix_bits;
+    const bfi_smp_row_params* params;
+    const uint32_t* hist;
+    const int64_t* hist_off;
+    const uint32_t* mask;
+    int64_t mask_stride;
+    const float* u;
+    uint32_t* out_tok;
+    // target introspection (all optional)
+    int32_t* t_kind;
+    int32_t* t_kept;
+    int32_t* t_listed;
+    uint32_t* t_ids;
+    float* t_probs;
+    int64_t t_cap;
+    float* t_stats;
+    // spec verify (rows_per_seq > 0)
+    int32_t rows_per_seq;
+    const uint32_t* drafts;
+    const int32_t* draft_len;
+    const float* u_pairs;
+    const float* u_bonus;
+    int32_t* out_accepted;
+    uint32_t* out_next;
+    // workspace
+    ChunkPart* parts;
+    Cand* cands;
+    uint32_t* row_ctr;
+    uint32_t* seq_ctr;
+    uint32_t* row_res;   // verify: 2 words per row {verdict, token}
+    uint32_t* row_pen;   // fallback select: per row bm[bm_words] + pre[bm_words] + cnt[GDCAP]
+    uint64_t* row_hist;  // fallback select: per row level-1 histogram (count, mass) x NBUCKET
+    int32_t bm_words;
+};
+
+// ---- atomics with an explicit address space ------------------------------------------
+// (generic-pointer atomics make the backend emit a runtime LDS/global test, which also
+// trips an instruction-selection bug; LDS atomics are workgroup-scoped, global ones agent)
+#define BFI_LDS __attribute__((address_space(3)))
+#define BFI_GLB __attribute__((address_space(1)))
+__device__ __forceinline__ uint32_t lds_add(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_add((BFI_LDS uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint32_t lds_or(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_or((BFI_LDS uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint64_t lds_add64(uint64_t* p, uint64_t v) {
+    return __hip_atomic_fetch_add((BFI_LDS uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint32_t glb_add(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_add((BFI_GLB uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t glb_or(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_or((BFI_GLB uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- float order key ------------------------------------------------------------------
+
+// Monotone map f32 -> u32 (larger float -> larger key). -0 folds onto +0 and NaN onto -inf,
+// so equal probabilities always have equal keys.
+__device__ __forceinline__ uint32_t ord32(float f) {
+    if (f != f) f = -__builtin_inff();
+    f = f + 0.0f;
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float unord32(uint32_t o) {
+    uint32_t u = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+    return __uint_as_float(u);
+}
+// Sort key of the reference order (sample.rs:393,398): descending value, ties by ascending
+// index (stable sort of an index-ordered list).
+__device__ __forceinline__ uint64_t key64(float s, uint32_t idx) {
+    return ((uint64_t)ord32(s) << 32) | (uint64_t)(~idx);
+}
+__device__ __forceinline__ uint32_t key_idx(uint64_t k) { return ~(uint32_t)k; }
+__device__ __forceinline__ float key_s(uint64_t k) { return unord32((uint32_t)(k >> 32)); }
+
+// ---- wave / block collectives ---------------------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        uint64_t w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Block reductions: `scr` is NWAVE words of LDS owned by the caller; both barriers are
+// inside, so calls may follow each other.
+__device__ __forceinline__ float block_max(float v, float* scr) {
+    v = wave_max(v);
+    if (lane_id() == 0) scr[wave_id()] = v;
+    __syncthreads();
+    float r = scr[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) r = fmaxf(r, scr[w]);
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ float block_sum(float v, float* scr) {
+    v = wave_sum(v);
+    if (lane_id() == 0) scr[wave_id()] = v;
+    __syncthreads();
+    float r = scr[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) r += scr[w];
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ double block_sum_d(double v, double* scr) {
+    v = wave_sum_d(v);
+    if (lane_id() == 0) scr[wave_id()] = v;
+    __syncthreads();
+    double r = scr[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) r += scr[w];
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ uint32_t block_sum_u(uint32_t v, uint32_t* scr) {
+    v = wave_sum_u(v);
+    if (lane_id() == 0) scr[wave_id()] = v;
+    __syncthreads();
+    uint32_t r = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) r += scr[w];
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ uint32_t block_min_u(uint32_t v, uint32_t* scr) {
+    v = wave_min_u(v);
+    if (lane_id() == 0) scr[wave_id()] = v;
+    __syncthreads();
+    uint32_t r = scr[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) r = min(r, scr[w]);
+    __syncthreads();
+    return r;
+}
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* scr) {
+    v = wave_max_u64(v);
+    if (lane_id() == 0) scr[wave_id()] = v;
+    __syncthreads();
+    uint64_t r = scr[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) r = scr[w] > r ? scr[w] : r;
+    __syncthreads();
+    return r;
+}
+
+// Exclusive block scan; `total` receives the block sum. Fixed combination order, so the
+// result is deterministic for floating-point T.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T* scr, T& total) {
+    T x = v;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        T y = __shfl_up(x, o);
+        if (lane_id() >= o) x += y;
+    }
+    if (lane_id() == WAVE - 1) scr[wave_id()] = x;
+    __syncthreads();
+    T pre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) {
+        T s = scr[w];
+        if (w < wave_id()) pre += s;
+        tot += s;
+    }
+    __syncthreads();
+    total = tot;
+    return pre + x - v;
+}
+
+// (value, index) argmax with the reference's tie rule (sample.rs:429-439): the first
+// (lowest) index of the maximum; NaN never wins.
+struct ArgMax {
+    float v;
+    uint32_t i;
+};
+__device__ __forceinline__ ArgMax argmax_merge(ArgMax a, ArgMax b) {
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+__device__ __forceinline__ ArgMax block_argmax(ArgMax a, float* scrv, uint32_t* scri) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        ArgMax b;
+        b.v = __shfl_xor(a.v, o);
+        b.i = __shfl_xor(a.i, o);
+        a = argmax_merge(a, b);
+    }
+    if (lane_id() == 0) {
+        scrv[wave_id()] = a.v;
+        scri[wave_id()] = a.i;
+    }
+    __syncthreads();
+    ArgMax r{scrv[0], scri[0]};
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) r = argmax_merge(r, ArgMax{scrv[w], scri[w]});
+    __syncthreads();
+    return r;
+}
+
+// ---- penalties: sample.rs:345-367 (+ frequency extension) ------------------------------
+
+struct Pen {
+    float rp, pp, fp;
+    bool rep_on, pres_on, freq_on;
+};
+
+__device__ __forceinline__ float penalize(float x, uint32_t count, const Pen& P) {
+    if (P.rep_on) x = (x > 0.0f) ? x / P.rp : x * P.rp;  // sample.rs:350-354
+    if (P.pres_on) x = x - P.pp;                          // sample.rs:364
+    if (P.freq_on) {                                      // extension: two roundings, no FMA
+        float fc = P.fp * (float)count;
+        x = x - fc;
+    }
+    return x;
+}
+
+// History of one row: the base ids plus (spec verify) the drafts accepted before this row.
+struct HistView {
+    const uint32_t* base;
+    int64_t nbase;
+    const uint32_t* extra;
+    int64_t nextra;
+    __device__ __forceinline__ int64_t size() const { return nbase + nextra; }
+    __device__ __forceinline__ uint32_t at(int64_t j) const {
+        return j < nbase ? base[j] : extra[j - nbase];
+    }
+    // Occurrences of id: slow path for rows whose distinct-id table overflowed.
+    __device__ __forceinline__ uint32_t count_scan(uint32_t id) const {
+        uint32_t c = 0;
+        for (int64_t j = 0; j < nbase; j++) c += base[j] == id;
+        for (int64_t j = 0; j < nextra; j++) c += extra[j] == id;
+        return c;
+    }
+};
+
+// Dense rank of bit b of word w among all set bits (word prefix + in-word popcount).
+__device__ __forceinline__ uint32_t dense_rank(uint32_t pre_w, uint32_t word, uint32_t b) {
+    return pre_w + __popc(word & ((1u << b) - 1u));
+}
+
+}  // namespace bfi

@@ -1,0 +1,200 @@
+// bfi_host.cpp — host-side helpers of the C ABI and the C++ mirror (bfi_host.hpp).
+#include "bfi_host.hpp"
+
+#include <cstring>
+
+extern "C" {
+
+uint64_t bfi_rng_next_u64(uint64_t* state) {  // sample.rs:445-455
+    uint64_t x = *state;
+    if (x == 0) x = 0x9E3779B97F4A7C15ull;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return x;
+}
+
+float bfi_rng_f32(uint64_t* state) {  // sample.rs:457-459
+    return (float)(bfi_rng_next_u64(state) >> 40) / (float)(1u << 24);
+}
+
+uint64_t bfi_slot_rng_seed(uint64_t seed, uint64_t prompt_len) {  // spec.rs:185-187
+    return seed ^ 0xa0761d6478bd642full ^ (prompt_len * 0x9e3779b97f4a7c15ull);
+}
+
+size_t bfi_draft(const uint32_t* ctx, size_t len, size_t k, size_t ngram_max, size_t ngram_min, uint32_t* out) {
+    // spec.rs:46-68: most recent earlier occurrence of the last n-gram, n = max..min
+    if (k == 0 || (len && !ctx) || !out) return 0;
+    const size_t lo = ngram_min > 1 ? ngram_min : 1;
+    for (size_t n = ngram_max; n >= lo && n > 0; n--) {
+        if (len < n + 1) continue;
+        const uint32_t* tail = ctx + (len - n);
+        for (size_t start = len - n; start-- > 0;) {
+            if (std::memcmp(ctx + start, tail, n * sizeof(uint32_t)) == 0) {
+                const size_t from = start + n;
+                const size_t to = from + k < len ? from + k : len;
+                if (from < to) {
+                    std::memcpy(out, ctx + from, (to - from) * sizeof(uint32_t));
+                    return to - from;
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+bool ws(char c) { return c == ' ' || c == '\t' || c == '\n' || c == '\r' || c == '\v' || c == '\f'; }
+
+std::string_view trim(std::string_view s) {
+    while (!s.empty() && ws(s.front())) s.remove_prefix(1);
+    while (!s.empty() && ws(s.back())) s.remove_suffix(1);
+    return s;
+}
+
+bool strip(std::string_view& s, std::string_view pre) {
+    if (s.substr(0, pre.size()) != pre) return false;
+    s.remove_prefix(pre.size());
+    return true;
+}
+
+// Rust `str::parse::<u32>()`: optional '+', ASCII digits, no overflow.
+bool parse_u32(std::string_view s, uint32_t& v) {
+    if (!s.empty() && s.front() == '+') s.remove_prefix(1);
+    if (s.empty()) return false;
+    uint64_t x = 0;
+    for (char c : s) {
+        if (c < '0' || c > '9') return false;
+        x = x * 10 + (uint64_t)(c - '0');
+        if (x > 0xFFFFFFFFull) return false;
+    }
+    v = (uint32_t)x;
+    return true;
+}
+
+}  // namespace
+
+extern "C" int bfi_parse_id_union(const char* grammar, int64_t n_vocab, uint32_t* mask_out) {
+    // sample.rs:207-221 parse_id_union, 231-235 strip_root
+    if (!grammar || n_vocab < 0 || (n_vocab > 0 && !mask_out)) return 0;
+    std::string_view s = trim(grammar);
+    if (!strip(s, "root")) return 0;
+    s = trim(s);
+    if (!strip(s, "::=")) return 0;
+    s = trim(s);
+    std::vector<uint32_t> ids;
+    for (;;) {
+        size_t bar = s.find('|');
+        std::string_view part = trim(s.substr(0, bar));
+        if (!strip(part, "id(") || part.empty() || part.back() != ')') return 0;
+        part.remove_suffix(1);
+        uint32_t id;
+        if (!parse_u32(trim(part), id)) return 0;
+        ids.push_back(id);
+        if (bar == std::string_view::npos) break;
+        s.remove_prefix(bar + 1);
+    }
+    if (ids.empty()) return 0;
+    const size_t words = (size_t)((n_vocab + 31) / 32);
+    std::memset(mask_out, 0, words * sizeof(uint32_t));
+    for (uint32_t id : ids)
+        if ((int64_t)id < n_vocab) mask_out[id >> 5] |= 1u << (id & 31);
+    return 1;
+}
+
+namespace bfi {
+
+std::vector<uint32_t> draft(const std::vector<uint32_t>& ctx, size_t k, size_t ngram_max, size_t ngram_min) {
+    std::vector<uint32_t> out(k);
+    out.resize(bfi_draft(ctx.data(), ctx.size(), k, ngram_max, ngram_min, out.data()));
+    return out;
+}
+
+std::optional<std::vector<uint32_t>> id_union_mask(const std::string& grammar, int64_t n_vocab) {
+    std::vector<uint32_t> m((size_t)((n_vocab + 31) / 32));
+    if (!bfi_parse_id_union(grammar.c_str(), n_vocab, m.data())) return std::nullopt;
+    return m;
+}
+
+Sampler::Sampler(int device) { check(bfi_smp_create(device, &ctx_)); }
+
+Sampler::~Sampler() { bfi_smp_destroy(ctx_); }
+
+void Sampler::check(int rc) {
+    if (rc != BFI_SMP_OK) throw Error(rc, bfi_smp_last_error(ctx_));
+}
+
+uint32_t Sampler::sample(const float* logits, size_t n_vocab, const uint32_t* prev, size_t n_prev,
+                         const SampleParams& p) {
+    std::optional<std::vector<uint32_t>> mask;
+    if (p.grammar) mask = id_union_mask(*p.grammar, (int64_t)n_vocab);
+    const bfi_smp_row_params row = p.row();
+    const float u = Rng(p.seed).f32();  // sample.rs:307 re-seeds every call
+    uint32_t tok = 0;
+    check(bfi_smp_sample_host(ctx_, logits, (int64_t)n_vocab, prev, (int64_t)n_prev, &row,
+                              mask ? mask->data() : nullptr, u, &tok));
+    return tok;
+}
+
+void Sampler::sample_rows(const void* d_logits, int dtype, int64_t n_rows, int64_t n_vocab, int64_t row_stride,
+                          const bfi_smp_row_params* d_params, const uint32_t* d_hist, const int64_t* d_hist_off,
+                          const uint32_t* d_mask, int64_t mask_stride, const float* d_u, uint32_t* d_out,
+                          void* stream) {
+    check(bfi_smp_sample_rows(ctx_, d_logits, dtype, n_rows, n_vocab, row_stride, d_params, d_hist, d_hist_off,
+                              d_mask, mask_stride, d_u, d_out, stream));
+}
+
+SpecReplay replay_spec(const std::vector<uint32_t>& drafted, int32_t kernel_accepted, uint32_t kernel_next,
+                       std::optional<uint32_t> eos, size_t generated, size_t max_tokens, Rng& rng) {
+    // spec.rs:140-162 with the verdicts already computed on the GPU
+    SpecReplay r;
+    std::optional<uint32_t> correction;
+    for (size_t i = 0; i < drafted.size(); i++) {
+        (void)rng.f32();  // u  (spec.rs:142)
+        (void)rng.f32();  // u2
+        if ((int32_t)i >= kernel_accepted) {  // Verdict::Reject(t)
+            correction = kernel_next;
+            break;
+        }
+        const uint32_t d = drafted[i];
+        if (eos && d == *eos) {  // Pushed::Eos: not appended, not counted
+            r.done = true;
+            break;
+        }
+        r.pushed.push_back(d);
+        r.accepted++;
+        if (generated + r.pushed.size() >= max_tokens) {  // budget_spent
+            r.done = true;
+            break;
+        }
+    }
+    if (!r.done) r.pending = correction;  // spec.rs:177-179
+    return r;
+}
+
+}  // namespace bfi
+
+// C entry point of replay_spec for callers without C++ (and the CPU tests).
+extern "C" int bfi_spec_replay(const uint32_t* drafted, size_t n_drafted, int32_t kernel_accepted,
+                               uint32_t kernel_next, int64_t eos, size_t generated, size_t max_tokens,
+                               uint64_t* rng_state, uint32_t* pushed_out, size_t* n_pushed, size_t* accepted,
+                               int* done, int64_t* pending) {
+    if ((n_drafted && !drafted) || !rng_state || !pushed_out || !n_pushed || !accepted || !done || !pending)
+        return BFI_SMP_EINVAL;
+    std::vector<uint32_t> d(drafted, drafted + n_drafted);
+    bfi::Rng rng(*rng_state);
+    std::optional<uint32_t> e;
+    if (eos >= 0) e = (uint32_t)eos;
+    bfi::SpecReplay r = bfi::replay_spec(d, kernel_accepted, kernel_next, e, generated, max_tokens, rng);
+    *rng_state = rng.state;
+    std::memcpy(pushed_out, r.pushed.data(), r.pushed.size() * sizeof(uint32_t));
+    *n_pushed = r.pushed.size();
+    *accepted = r.accepted;
+    *done = r.done ? 1 : 0;
+    *pending = r.pending ? (int64_t)*r.pending : -1;
+    return BFI_SMP_OK;
+}

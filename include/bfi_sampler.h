@@ -79,6 +79,13 @@ void bfi_smp_destroy(bfi_smp_ctx *ctx);
 const char *bfi_smp_last_error(const bfi_smp_ctx *ctx);
 int bfi_smp_abi_version(void);
 
+/* Profiling (no counterpart in the reference; for benchmarks): while enabled, every launch
+ * records HIP events on the caller's stream around its two kernels (the streaming pass over
+ * the logits, then the per-row selection). bfi_smp_profile waits for the recorded launches,
+ * returns the summed event times in ms and clears the record (at most 65536 launches). */
+int bfi_smp_set_profiling(bfi_smp_ctx *ctx, int enabled);
+int bfi_smp_profile(bfi_smp_ctx *ctx, double *stream_ms, double *select_ms, int64_t *launches);
+
 /* ---- batched sampling: generate_batch's per-step call ------------------- */
 
 /*
@@ -174,6 +181,16 @@ size_t bfi_draft(const uint32_t *ctx_ids, size_t len, size_t k, size_t ngram_max
  * Returns 1 when `grammar` is an id union (mask written; ids >= n_vocab ignored), 0 when
  * it is not (mask untouched). */
 int bfi_parse_id_union(const char *grammar, int64_t n_vocab, uint32_t *mask_out);
+
+/* Host half of take_token_spec after a GPU verify (spec.rs:140-179): replays the stop
+ * rules (EOS never appended, budget `max_tokens` counting `generated` tokens so far) over
+ * the kernel's verdicts for one sequence and advances the slot RNG by two draws per judged
+ * row. eos < 0 means no EOS id. Outputs: pushed ids, accepted count (SpecStats::accepted),
+ * done flag, pending correction (-1 = none). */
+int bfi_spec_replay(const uint32_t *drafted, size_t n_drafted, int32_t kernel_accepted,
+                    uint32_t kernel_next, int64_t eos, size_t generated, size_t max_tokens,
+                    uint64_t *rng_state, uint32_t *pushed_out, size_t *n_pushed, size_t *accepted,
+                    int *done, int64_t *pending);
 
 #ifdef __cplusplus
 } /* extern "C" */

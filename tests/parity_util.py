@@ -1,0 +1,97 @@
+"""Comparison of GPU results with the CPU oracle under the parity bar of the sampling path.
+
+Token ids must equal the oracle's. The only exemption is a draw whose u lies within 1e-6
+of a CDF boundary, and it is checked constructively: the oracle, re-run with some
+u' in [u - 1e-6, u + 1e-6], must return the GPU's token. Kept sets must be equal, except at
+a top-p boundary, where the exact (float64) cumulative mass at the cut is within BAND of
+top_p. In that case the reference's own float32 sequential sum decides the cut. Probabilities
+must agree within 1e-5 relative, or within 2e-6 relative of the float64 value when the
+reference's sequential float32 normalizer is itself off by more than that.
+"""
+import numpy as np
+
+import oracle as O
+
+U_TOL = 1e-6
+BAND = 1e-5
+P_RTOL = 1e-5
+
+
+def u_grid(u):
+    return [float(np.float32(u + d)) for d in np.linspace(-U_TOL, U_TOL, 9)]
+
+
+def exact_probs(s):
+    s = s.astype(np.float64)
+    m = np.max(s)
+    if not np.isfinite(m):
+        return None
+    e = np.exp(s - m)
+    return e / e.sum()
+
+
+def top_p_band(s, top_p, lens):
+    """True when the float64 cumulative mass near the cut is within BAND of top_p."""
+    pr = exact_probs(s)
+    if pr is None:
+        return False
+    order = np.argsort(-pr, kind="stable")
+    cum = np.cumsum(pr[order])
+    lo, hi = max(min(lens) - 2, 0), min(max(lens), len(cum))
+    return bool(np.any(np.abs(cum[lo:hi] - top_p) <= BAND))
+
+
+def compare_target(cfg, gpu, orc, logits_f32=None, check_list=True):
+    """gpu/orc: dicts of numpy arrays from target_rows. Returns (problems, stats)."""
+    B = cfg["B"]
+    prm = cfg["params"]
+    problems, stats = [], dict(rows=B, u_exempt=0, band_exempt=0, listed_rows=0)
+    for b in range(B):
+        p = {k: float(prm[b][k]) if k != "top_k" else int(prm[b][k]) for k in prm.dtype.names if k != "reserved"}
+        ok_, gk = int(orc["kind"][b]), int(gpu["kind"][b])
+        if ok_ != gk:
+            problems.append(f"row {b}: kind gpu={gk} oracle={ok_}")
+            continue
+        tok_g, tok_o = int(gpu["token"][b]), int(orc["token"][b])
+        if ok_ == 0:
+            if tok_g != tok_o:
+                problems.append(f"row {b}: token target gpu={tok_g} oracle={tok_o}")
+            continue
+        kl_o, kl_g = int(orc["kept_len"][b]), int(gpu["kept_len"][b])
+        band = False
+        if kl_o != kl_g:
+            if p["top_p"] < 1.0 and orc.get("s") is not None and top_p_band(orc["s"][b], p["top_p"], (kl_o, kl_g)):
+                band = True
+                stats["band_exempt"] += 1
+            else:
+                problems.append(f"row {b}: kept_len gpu={kl_g} oracle={kl_o} params={p}")
+                continue
+        listed = int(gpu["listed"][b])
+        if check_list and listed > 0 and not band:
+            stats["listed_rows"] += 1
+            ref_ids = orc["ids"][b, :kl_o]
+            ref_w = orc["probs"][b, :kl_o]
+            nz = ref_w > 0
+            ri, rw = ref_ids[nz], ref_w[nz]
+            gi, gw = gpu["ids"][b, :listed].astype(np.uint32), gpu["probs"][b, :listed]
+            n = min(len(ri), len(gi))
+            if len(gi) != min(len(ri), gpu["ids"].shape[1]) or not np.array_equal(gi[:n], ri[:n]):
+                first = int(np.argmax(gi[:n] != ri[:n])) if n and not np.array_equal(gi[:n], ri[:n]) else n
+                problems.append(f"row {b}: kept list differs at {first} (gpu {len(gi)} vs oracle {len(ri)}) params={p}")
+                continue
+            rel = np.abs(gw[:n] - rw[:n]) / np.maximum(rw[:n], 1e-38)
+            if np.any(rel > P_RTOL):
+                ex = exact_probs(orc["s"][b]) if orc.get("s") is not None else None
+                bad = np.nonzero(rel > P_RTOL)[0]
+                if ex is None or np.any(np.abs(gw[bad] - ex[gi[bad]]) / ex[gi[bad]] > 2e-6):
+                    problems.append(f"row {b}: prob rel err {rel.max():.3g} at {int(bad[0])}")
+                    continue
+        if tok_g != tok_o:
+            x = logits_f32[b] if logits_f32 is not None else None
+            hist = cfg["hist"][cfg["hist_off"][b]:cfg["hist_off"][b + 1]]
+            mask = None if cfg["mask"] is None else cfg["mask"][b]
+            if x is not None and any(O.sample(x, hist, p, mask, uu) == tok_g for uu in u_grid(cfg["u"][b])):
+                stats["u_exempt"] += 1
+            else:
+                problems.append(f"row {b}: token gpu={tok_g} oracle={tok_o} u={cfg['u'][b]} params={p}")
+    return problems, stats
