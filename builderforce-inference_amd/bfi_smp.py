@@ -55,6 +55,9 @@ def lib():
         L.bfi_smp_last_error.argtypes = [P]
         L.bfi_smp_last_error.restype = ctypes.c_char_p
         L.bfi_smp_abi_version.restype = I32
+        L.bfi_smp_set_tracing.argtypes = [P, I32]
+        L.bfi_smp_trace.argtypes = [P, P, I64]
+        L.bfi_smp_trace.restype = I64
         L.bfi_smp_set_profiling.argtypes = [P, I32]
         L.bfi_smp_profile.argtypes = [P, P, P, P]
         L.bfi_smp_sample_rows.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P]
@@ -180,6 +183,16 @@ class Sampler:
 
             return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         return ctypes.c_void_p(stream)
+
+    def set_tracing(self, on: bool):
+        self._check(self._L.bfi_smp_set_tracing(self._ctx, 1 if on else 0), "bfi_smp_set_tracing")
+
+    def trace(self, max_words=1 << 22):
+        out = np.zeros(max_words, np.uint64)
+        n = self._L.bfi_smp_trace(self._ctx, _np_ptr(out), max_words)
+        if n < 0:
+            raise SamplerError("bfi_smp_trace failed")
+        return out[:n]
 
     def set_profiling(self, on: bool):
         self._check(self._L.bfi_smp_set_profiling(self._ctx, 1 if on else 0), "bfi_smp_set_profiling")

@@ -30,6 +30,10 @@ struct bfi_smp_ctx {
     // staging for bfi_smp_sample_host
     char* stage = nullptr;
     size_t stage_size = 0;
+    // phase trace of the last launch (diagnostics)
+    uint64_t* trace = nullptr;
+    size_t trace_words = 0, trace_used = 0;
+    bool tracing = false;
     // profiling: event triples around (k_stream, k_select) of each launch
     bool profiling = false;
     std::vector<hipEvent_t> ev_pool;
@@ -262,6 +266,22 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     a.row_ctr = ctx->ctr;
     a.seq_ctr = ctx->ctr + c.n_rows;
     a.bm_words = bm_words;
+    a.trace = nullptr;
+    if (ctx->tracing) {
+        size_t words = ((size_t)c.n_rows * s.n_chunks + (size_t)c.n_rows) * 8;
+        if (words > ctx->trace_words) {
+            if (ctx->trace) (void)hipFree(ctx->trace);
+            ctx->trace = nullptr;
+            ctx->trace_words = 0;
+            if (hipMalloc((void**)&ctx->trace, words * 8) != hipSuccess)
+                return fail(ctx, BFI_SMP_ENOMEM, "trace allocation failed");
+            ctx->trace_words = words;
+        }
+        hipError_t e0 = hipMemsetAsync(ctx->trace, 0, words * 8, stream);
+        if (e0 != hipSuccess) return hip_fail(ctx, e0, "hipMemsetAsync(trace)");
+        ctx->trace_used = words;
+        a.trace = ctx->trace;
+    }
 
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     if (ctx->profiling) {
@@ -322,6 +342,20 @@ void bfi_smp_destroy(bfi_smp_ctx* ctx) {
         if (ctx->stage) (void)hipFree(ctx->stage);
     }
     delete ctx;
+}
+
+int bfi_smp_set_tracing(bfi_smp_ctx* ctx, int enabled) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    ctx->tracing = enabled != 0;
+    return BFI_SMP_OK;
+}
+
+int64_t bfi_smp_trace(bfi_smp_ctx* ctx, uint64_t* out, int64_t max_words) {
+    if (!ctx || !out || max_words < 0) return -1;
+    DeviceGuard g(ctx->device);
+    size_t n = ctx->trace_used < (size_t)max_words ? ctx->trace_used : (size_t)max_words;
+    if (n && hipMemcpy(out, ctx->trace, n * 8, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return (int64_t)n;
 }
 
 int bfi_smp_set_profiling(bfi_smp_ctx* ctx, int enabled) {

@@ -16,7 +16,7 @@ constexpr int BLOCK = 256;  // threads per workgroup (4 wave64s)
 constexpr int WAVE = 64;
 constexpr int NWAVE = BLOCK / WAVE;
 constexpr int CHUNK_MAX = 8192;        // logits elements per workgroup (stream phase)
-constexpr int CAND_CAP = 512;          // candidates one chunk may hand to the combine
+constexpr int CAND_CAP = 2048;         // candidates one chunk may hand to the combine
 constexpr int NMAX = 2048;             // combine sort capacity (power of two)
 constexpr int NBUCKET = 1024;          // radix buckets (10-bit digits) of the fallback select
 constexpr int DCAP = 1024;             // distinct history ids counted per chunk in LDS
@@ -84,7 +84,14 @@ struct KArgs {
     uint32_t* row_pen;   // fallback select: per row bm[bm_words] + pre[bm_words] + cnt[GDCAP]
     uint64_t* row_hist;  // fallback select: per row level-1 histogram (count, mass) x NBUCKET
     int32_t bm_words;
+    uint64_t* trace;  // optional phase timestamps (wall clock) per workgroup
 };
+
+// Phase timestamp of a workgroup (diagnostics; no-op without a trace buffer).
+#define BFI_TRACE(a, base, i)                                                            \
+    do {                                                                                 \
+        if ((a).trace && threadIdx.x == 0) (a).trace[(base) + (i)] = wall_clock64();     \
+    } while (0)
 
 // ---- atomics with an explicit address space ------------------------------------------
 // (generic-pointer atomics make the backend emit a runtime LDS/global test, which also
@@ -168,6 +175,34 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+// Bitonic sort of one key per lane across the wave, descending (lane 0 = largest).
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= WAVE; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint64_t other = __shfl_xor(key, stride);
+            const bool desc = (lane & size) == 0 || size == WAVE;
+            const bool lower = (lane & stride) == 0;
+            const bool take_max = lower == desc;
+            const uint64_t mx = other > key ? other : key, mn = other > key ? key : other;
+            key = take_max ? mx : mn;
+        }
+    }
+    return key;
+}
+__device__ __forceinline__ double wave_incl_scan_d(double v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        double y = __shfl_up(v, o);
+        if (lane >= o) v += y;
+    }
+    return v;
+}
+__device__ __forceinline__ uint64_t lanes_below() { return (1ull << lane_id()) - 1ull; }
+
 // Block reductions: `scr` is NWAVE words of LDS owned by the caller; both barriers are
 // inside, so calls may follow each other.
 __device__ __forceinline__ float block_max(float v, float* scr) {
@@ -208,6 +243,26 @@ __device__ __forceinline__ uint32_t block_sum_u(uint32_t v, uint32_t* scr) {
 #pragma unroll
     for (int w = 0; w < NWAVE; w++) r += scr[w];
     __syncthreads();
+    return r;
+}
+// Sum of a float and of a count in one pair of barriers.
+__device__ __forceinline__ float block_sum_fu(float v, uint32_t c, uint32_t& csum, float* scrf, uint32_t* scru) {
+    v = wave_sum(v);
+    c = wave_sum_u(c);
+    if (lane_id() == 0) {
+        scrf[wave_id()] = v;
+        scru[wave_id()] = c;
+    }
+    __syncthreads();
+    float r = scrf[0];
+    uint32_t rc = scru[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) {
+        r += scrf[w];
+        rc += scru[w];
+    }
+    __syncthreads();
+    csum = rc;
     return r;
 }
 __device__ __forceinline__ uint32_t block_min_u(uint32_t v, uint32_t* scr) {

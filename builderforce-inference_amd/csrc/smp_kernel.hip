@@ -76,7 +76,8 @@ struct RowCtx {
     bool active, verify, judged;
     uint32_t draft;
     float u, u2;
-    float T, top_p, min_p;
+    float T, rT, top_p, min_p;
+    bool fast_div;  // T in [2^-20, 2^20]: FMA-corrected reciprocal division is exact
     int32_t k;
     bool greedy, kmode, pmode, mmode;
     Pen pen;
@@ -133,6 +134,8 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
     }
     const int64_t H = C.h.size();
     C.T = P.temperature;
+    C.rT = 1.0f / P.temperature;  // IEEE, once per row
+    C.fast_div = P.temperature >= 0x1p-20f && P.temperature <= 0x1p20f;
     C.top_p = P.top_p;
     C.min_p = P.min_p;
     C.k = P.top_k;
@@ -172,7 +175,25 @@ struct Elem<true> {
 };
 
 // Loads the elements thread `tid` owns in [c0, c1): vector q covers ids
-// c0 + (q*BLOCK + tid)*EPV + [0, EPV). Out-of-range elements read as -inf.
+// c0 + (q*BLOCK + tid)*EPV + [0, EPV). Out-of-range elements read as -inf. A full, aligned
+// tile takes only unconditional 16-byte loads, so all VEC loads are in flight together.
+template <bool BF16, int VEC>
+__device__ __forceinline__ void unpack16(const uint4 w, float (&v)[Elem<BF16>::EPV]) {
+    if (!BF16) {
+        v[0] = __uint_as_float(w.x);
+        v[1] = __uint_as_float(w.y);
+        v[2] = __uint_as_float(w.z);
+        v[3] = __uint_as_float(w.w);
+    } else {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[2 * e] = __uint_as_float(ww[e] << 16);
+            v[2 * e + 1] = __uint_as_float(ww[e] & 0xFFFF0000u);
+        }
+    }
+}
+
 template <bool BF16, int VEC>
 __device__ __forceinline__ void load_tile(const KArgs& a, int row, uint32_t c0, uint32_t c1,
                                           float (&x)[VEC][Elem<BF16>::EPV]) {
@@ -180,24 +201,19 @@ __device__ __forceinline__ void load_tile(const KArgs& a, int row, uint32_t c0, 
     typedef typename Elem<BF16>::T T;
     const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
     const int tid = threadIdx.x;
+    if (a.vec_ok && c1 - c0 == (uint32_t)(BLOCK * VEC * EPV)) {
+        uint4 w[VEC];
+#pragma unroll
+        for (int q = 0; q < VEC; q++) w[q] = *(const uint4*)(base + c0 + (uint32_t)(q * BLOCK + tid) * EPV);
+#pragma unroll
+        for (int q = 0; q < VEC; q++) unpack16<BF16, VEC>(w[q], x[q]);
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < VEC; q++) {
         const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
         if (a.vec_ok && id0 + EPV <= c1) {
-            const uint4 w = *(const uint4*)(base + id0);
-            if (!BF16) {
-                x[q][0] = __uint_as_float(w.x);
-                x[q][1] = __uint_as_float(w.y);
-                x[q][2] = __uint_as_float(w.z);
-                x[q][3] = __uint_as_float(w.w);
-            } else {
-                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    x[q][2 * e] = __uint_as_float(ww[e] << 16);
-                    x[q][2 * e + 1] = __uint_as_float(ww[e] & 0xFFFF0000u);
-                }
-            }
+            unpack16<BF16, VEC>(*(const uint4*)(base + id0), x[q]);
         } else {
 #pragma unroll
             for (int e = 0; e < EPV; e++)
@@ -208,9 +224,24 @@ __device__ __forceinline__ void load_tile(const KArgs& a, int row, uint32_t c0, 
 
 // ---- history structures ----------------------------------------------------------------
 
+// The first 2*BLOCK history ids of a row, loaded into registers before the logits so that
+// their latency overlaps the HBM stream (UINT32_MAX past the end).
+struct HistPre {
+    uint32_t v0, v1;
+};
+__device__ __forceinline__ HistPre hist_prefetch(const RowCtx& C) {
+    const int64_t H = C.h.size();
+    const int tid = threadIdx.x;
+    HistPre p;
+    p.v0 = (C.pen_on && tid < H) ? C.h.at(tid) : 0xFFFFFFFFu;
+    p.v1 = (C.pen_on && tid + BLOCK < H) ? C.h.at(tid + BLOCK) : 0xFFFFFFFFu;
+    return p;
+}
+
 // Chunk-local history bitmap + dense occurrence counts in LDS (ids in [c0, c1)).
 template <typename SM>
-__device__ __forceinline__ void build_chunk_pen(SM& sm, const RowCtx& C, uint32_t c0, uint32_t c1) {
+__device__ __forceinline__ void build_chunk_pen(SM& sm, const RowCtx& C, uint32_t c0, uint32_t c1,
+                                                HistPre hp) {
     const int tid = threadIdx.x;
     const uint32_t nw = (c1 - c0 + 31) / 32;
     for (uint32_t w = tid; w < CHUNK_MAX / 32; w += BLOCK) sm.u.st.bm[w] = 0;
@@ -218,7 +249,9 @@ __device__ __forceinline__ void build_chunk_pen(SM& sm, const RowCtx& C, uint32_
         for (uint32_t w = tid; w < DCAP; w += BLOCK) sm.u.st.cnt[w] = 0;
     __syncthreads();
     const int64_t H = C.h.size();
-    for (int64_t j = tid; j < H; j += BLOCK) {
+    if (hp.v0 >= c0 && hp.v0 < c1) lds_or(&sm.u.st.bm[(hp.v0 - c0) >> 5], 1u << ((hp.v0 - c0) & 31));
+    if (hp.v1 >= c0 && hp.v1 < c1) lds_or(&sm.u.st.bm[(hp.v1 - c0) >> 5], 1u << ((hp.v1 - c0) & 31));
+    for (int64_t j = tid + 2 * BLOCK; j < H; j += BLOCK) {
         uint32_t id = C.h.at(j);
         if (id >= c0 && id < c1) lds_or(&sm.u.st.bm[(id - c0) >> 5], 1u << ((id - c0) & 31));
     }
@@ -231,13 +264,15 @@ __device__ __forceinline__ void build_chunk_pen(SM& sm, const RowCtx& C, uint32_
         if (tid == 0) sm.misc[MISC_NDIST] = tot;
         __syncthreads();
         if (tot <= DCAP) {
-            for (int64_t j = tid; j < H; j += BLOCK) {
-                uint32_t id = C.h.at(j);
+            auto count = [&](uint32_t id) {
                 if (id >= c0 && id < c1) {
                     uint32_t o = id - c0, w = o >> 5;
                     lds_add(&sm.u.st.cnt[dense_rank(sm.u.st.pre[w], sm.u.st.bm[w], o & 31)], 1u);
                 }
-            }
+            };
+            count(hp.v0);
+            count(hp.v1);
+            for (int64_t j = tid + 2 * BLOCK; j < H; j += BLOCK) count(C.h.at(j));
         }
         __syncthreads();
     }
@@ -327,30 +362,75 @@ __device__ __forceinline__ uint32_t pen_count(const SM& sm, const PenSrc& S, con
     return S.gcnt[dense_rank(S.gpre[id >> 5], S.gbm[id >> 5], id & 31)];
 }
 
+// x / T rounded like IEEE division (sample.rs:373-375). With r = RN(1/T), q = RN(x*r) is
+// within one ulp of x/T, e = x - q*T is exact under FMA, and RN(q + e*r) is the correctly
+// rounded quotient while no step underflows or overflows (Markstein's correction). This was
+// checked bit-exhaustively against IEEE division over all f32 x with |x| in [2^-100, 2^100]
+// for temperatures across [2^-20, 2^20]. Zeros give +-0 and infinities/NaN pass through (e
+// is NaN there, and q is already the quotient). `div_ok` says whether x is in the checked
+// range; a wave with any other value takes IEEE division for its whole tile.
+__device__ __forceinline__ float div_T_fast(float x, const RowCtx& C) {
+    const float q = x * C.rT;
+    const float e = __builtin_fmaf(-q, C.T, x);
+    const float s = __builtin_fmaf(e, C.rT, q);
+    return e != e ? q : s;
+}
+__device__ __forceinline__ bool div_ok(float x) {
+    const uint32_t a = __float_as_uint(x) & 0x7FFFFFFFu;
+    // bad: nonzero below 2^-100, or finite at/above 2^100
+    return !((a - 1u < 0x0D7FFFFFu) || (a - 0x71800000u < 0x0E000000u));
+}
+__device__ __forceinline__ float div_T(float x, const RowCtx& C) {
+    return (C.fast_div && div_ok(x)) ? div_T_fast(x, C) : x / C.T;
+}
+
 // In place: masked -> penalized -> (/T unless greedy). Tracks the masked, un-penalized
-// argmax when `raw` is non-null (min-p fallback, sample.rs:415-422).
+// argmax when RAW (min-p fallback, sample.rs:415-422).
 template <bool BF16, int VEC, bool RAW = false, typename SM>
 __device__ __forceinline__ ArgMax transform_tile(const SM& sm, const RowCtx& C, const PenSrc& S,
-                                               uint32_t c0, uint32_t c1,
-                                               float (&x)[VEC][Elem<BF16>::EPV]) {
+                                                 uint32_t c0, uint32_t c1,
+                                                 float (&x)[VEC][Elem<BF16>::EPV]) {
     constexpr int EPV = Elem<BF16>::EPV;
     const int tid = threadIdx.x;
     const uint32_t em = (1u << EPV) - 1u;
     ArgMax raw{-__builtin_inff(), 0xFFFFFFFFu};
+    bool bad = false;
 #pragma unroll
     for (int q = 0; q < VEC; q++) {
         const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
         if (id0 >= c1) continue;  // all -inf already
-        uint32_t mb = em;
-        if (C.mrow) mb = (C.mrow[id0 >> 5] >> (id0 & 31)) & em;
-        uint32_t pb = C.pen_on ? pen_bits(sm, S, id0, EPV) : 0u;
+        if (C.mrow) {             // sample.rs:331-337
+            const uint32_t mb = (C.mrow[id0 >> 5] >> (id0 & 31)) & em;
 #pragma unroll
-        for (int e = 0; e < EPV; e++) {
-            float v = ((mb >> e) & 1u) ? x[q][e] : -__builtin_inff();  // sample.rs:331-337
-            if (RAW && id0 + e < c1) raw = argmax_merge(raw, ArgMax{v, id0 + e});
-            if ((pb >> e) & 1u) v = penalize(v, pen_count(sm, S, C, id0 + e), C.pen);
-            if (!C.greedy) v = v / C.T;  // sample.rs:373-375, IEEE division
-            x[q][e] = v;
+            for (int e = 0; e < EPV; e++) x[q][e] = ((mb >> e) & 1u) ? x[q][e] : -__builtin_inff();
+        }
+        if (RAW) {
+#pragma unroll
+            for (int e = 0; e < EPV; e++)
+                if (id0 + e < c1) raw = argmax_merge(raw, ArgMax{x[q][e], id0 + e});
+        }
+        const uint32_t pb = C.pen_on ? pen_bits(sm, S, id0, EPV) : 0u;
+        if (pb) {  // rare: an id of the history in this vector
+#pragma unroll
+            for (int e = 0; e < EPV; e++)
+                if ((pb >> e) & 1u) x[q][e] = penalize(x[q][e], pen_count(sm, S, C, id0 + e), C.pen);
+        }
+        if (!C.greedy) {
+#pragma unroll
+            for (int e = 0; e < EPV; e++) bad = bad || !div_ok(x[q][e]);
+        }
+    }
+    if (!C.greedy) {  // sample.rs:373-375
+        if (C.fast_div && __ballot(bad) == 0) {
+#pragma unroll
+            for (int q = 0; q < VEC; q++)
+#pragma unroll
+                for (int e = 0; e < EPV; e++) x[q][e] = div_T_fast(x[q][e], C);
+        } else {
+#pragma unroll
+            for (int q = 0; q < VEC; q++)
+#pragma unroll
+                for (int e = 0; e < EPV; e++) x[q][e] = x[q][e] / C.T;
         }
     }
     return raw;
@@ -493,9 +573,115 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t* k, int n) {
 
 // ---- combine: bounded candidates -------------------------------------------------------
 
+// The bounded combine for N <= 64 candidates (in sm.u.cb.keys): wave 0 does all of it in
+// registers with shuffles and ballots, no barrier; the others wait for the result.
+__device__ __forceinline__ void combine_wave(const KArgs& a, Smem& sm, const RowCtx& C, int N, bool sorted, float M,
+                                             float S, ArgMax rawmax) {
+    enum { R_TOK = 0, R_VERDICT = 1, R_TOKEN_TARGET = 2 };
+    if (wave_id() == 0) {
+        const int lane = lane_id();
+        const bool valid = lane < N;
+        uint64_t key = valid ? sm.u.cb.keys[lane] : 0ull;
+        key = wave_sort_desc(key);
+        const float s = sorted ? key_s(key) : unord32((uint32_t)key);
+        const uint32_t idx = sorted ? key_idx(key) : ~(uint32_t)(key >> 32);
+        const float p = valid ? expf(s - M) / S : 0.0f;  // sample.rs:383, 388
+        const int64_t Lk = C.kmode ? C.k : a.V;
+        const int lim = (int)(Lk < N ? Lk : N);
+        int64_t Lp = INT64_MAX, Lm = INT64_MAX;
+        if (sorted && C.pmode) {  // sample.rs:397-409
+            const double cum = wave_incl_scan_d((double)p);
+            const uint64_t hit = __ballot(lane < lim && cum >= (double)C.top_p);
+            Lp = hit ? (int64_t)__ffsll((unsigned long long)hit) : Lk;
+        }
+        float thresh = 0.0f;
+        bool token_target = false;
+        uint32_t tok = 0, verdict = 1;
+        if (C.mmode) {  // sample.rs:411-414
+            thresh = C.min_p * (1.0f / S);
+            if (sorted) {
+                const int lim2 = (int)(Lp < lim ? Lp : lim);
+                const uint64_t fail = __ballot(lane < lim2 && p < thresh);
+                Lm = fail ? (int64_t)__ffsll((unsigned long long)fail) - 1 : lim2;
+            } else {
+                Lm = __popcll(__ballot(valid && p >= thresh));
+            }
+            if (Lm == 0) {  // sample.rs:415-422
+                token_target = true;
+                tok = rawmax.v > -__builtin_inff() ? rawmax.i : 0u;
+                verdict = C.judged ? (tok == C.draft) : 1u;
+            }
+        }
+        if (!token_target) {
+            const int64_t L = sorted ? min(Lk, min(Lp, Lm)) : Lm;
+            const int nl = sorted ? (int)(L < N ? L : N) : N;
+            const bool kept = sorted ? lane < nl : (valid && p >= thresh);
+            if (a.t_kind) {
+                const bool listed = kept && p > 0.0f;
+                const uint64_t lm = __ballot(listed);
+                const int o = __popcll(lm & lanes_below());
+                if (listed && o < a.t_cap) {
+                    a.t_ids[(int64_t)C.row * a.t_cap + o] = idx;
+                    a.t_probs[(int64_t)C.row * a.t_cap + o] = p;
+                }
+                if (lane == 0) {
+                    a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
+                    a.t_kept[C.row] = (int32_t)L;
+                    a.t_listed[C.row] = (int32_t)min((int64_t)__popcll(lm), a.t_cap);
+                }
+            }
+            const double w = kept ? (double)p : 0.0;
+            const double cumk = wave_incl_scan_d(w);
+            const double sum = __shfl(cumk, WAVE - 1);
+            if (!C.judged) {  // draw, sample.rs:312-323
+                const double r = (double)C.u * sum;
+                const uint64_t hit = __ballot(kept && cumk >= r);
+                const int j = hit ? __ffsll((unsigned long long)hit) - 1 : 0;
+                tok = __shfl(idx, j);
+            } else {  // judge, spec.rs:83-95
+                const uint64_t dm = __ballot(kept && idx == C.draft);
+                const int pd = dm ? __ffsll((unsigned long long)dm) - 1 : -1;
+                const double p_d = pd >= 0 ? (double)__shfl(p, pd) : 0.0;
+                if (sum > 0.0 && (double)C.u < p_d / sum) {
+                    tok = C.draft;
+                    verdict = 1;
+                } else {
+                    const bool res = kept && lane != pd;
+                    if (__ballot(res && p > 0.0f) == 0) {  // residual empty or all <= 0
+                        tok = C.draft;
+                        verdict = 1;
+                    } else {
+                        const double cum2 = wave_incl_scan_d(res ? (double)p : 0.0);
+                        const double r2 = (double)C.u2 * (sum - p_d);
+                        const uint64_t hit = __ballot(res && cum2 >= r2);
+                        const int j = hit ? __ffsll((unsigned long long)hit) - 1 : 0;
+                        tok = __shfl(idx, j);
+                        verdict = 0;
+                    }
+                }
+            }
+        }
+        if (lane == 0) {
+            sm.misc[4 + R_TOK] = tok;
+            sm.misc[4 + R_VERDICT] = verdict;
+            sm.misc[4 + R_TOKEN_TARGET] = token_target;
+        }
+    }
+    __syncthreads();
+    const uint32_t tok = sm.misc[4 + R_TOK], verdict = sm.misc[4 + R_VERDICT];
+    const bool token_target = sm.misc[4 + R_TOKEN_TARGET] != 0;
+    __syncthreads();
+    if (token_target) {
+        finish_token(a, sm, C, tok);
+        return;
+    }
+    if (a.t_kind && threadIdx.x == 0 && a.out_tok) a.out_tok[C.row] = tok;
+    emit(a, sm, C, tok, verdict);
+}
+
 // Returns false when the candidates do not fit (caller falls back to the radix select).
 __device__ __forceinline__ bool combine_bounded(const KArgs& a, Smem& sm, const RowCtx& C, const ChunkPart& mine,
-                                float M, float S, ArgMax rawmax) {
+                                float M, float S, ArgMax rawmax, int64_t tb) {
     const int tid = threadIdx.x;
     const int nc = a.n_chunks;
     const bool sorted = C.kmode || C.pmode;  // else min-p only: index order (sample.rs:411-414)
@@ -507,8 +693,8 @@ __device__ __forceinline__ bool combine_bounded(const KArgs& a, Smem& sm, const 
         float margin = 1e-4f + 1e-5f * (fabsf(M) + fabsf(lm));
         theta = fmaxf(theta, M + lm - margin);
     }
-    // prefix of candidate counts over chunks
-    uint32_t myn = tid < nc ? mine.ncand : 0u;
+    // prefix of candidate counts over chunks (a chunk whose max is below theta has none)
+    uint32_t myn = (tid < nc && mine.m >= theta) ? mine.ncand : 0u;
     uint32_t tot;
     uint32_t off = block_excl_scan<uint32_t>(myn, sm.ru, tot);
     if (tid < nc) sm.cpre[tid] = off;
@@ -518,29 +704,49 @@ __device__ __forceinline__ bool combine_bounded(const KArgs& a, Smem& sm, const 
     }
     __syncthreads();
     const Cand* cands = a.cands + (int64_t)C.row * nc * CAND_CAP;
-    for (uint32_t f = tid; f < tot; f += BLOCK) {
-        int lo = 0, hi = nc;  // largest c with cpre[c] <= f
-        while (hi - lo > 1) {
-            int mid = (lo + hi) >> 1;
-            if (sm.cpre[mid] <= f) lo = mid;
-            else hi = mid;
+    constexpr int GU = 4;  // loads in flight per thread
+    for (uint32_t f0 = tid; f0 < tot; f0 += GU * BLOCK) {
+        Cand cd[GU];
+#pragma unroll
+        for (int g = 0; g < GU; g++) {
+            const uint32_t f = f0 + g * BLOCK;
+            cd[g].idx = 0;
+            cd[g].s = -__builtin_inff();
+            if (f < tot) {
+                int lo = 0, hi = nc;  // largest c with cpre[c] <= f
+                while (hi - lo > 1) {
+                    int mid = (lo + hi) >> 1;
+                    if (sm.cpre[mid] <= f) lo = mid;
+                    else hi = mid;
+                }
+                cd[g] = cands[(int64_t)lo * CAND_CAP + (f - sm.cpre[lo])];
+            }
         }
-        Cand cd = cands[(int64_t)lo * CAND_CAP + (f - sm.cpre[lo])];
-        if (cd.s >= theta && cd.s > -__builtin_inff()) {
-            uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
-            if (slot < NMAX)
-                sm.u.cb.keys[slot] = sorted ? key64(cd.s, cd.idx)
-                                            : (((uint64_t)(~cd.idx) << 32) | ord32(cd.s));
+#pragma unroll
+        for (int g = 0; g < GU; g++) {
+            if (cd[g].s >= theta && cd[g].s > -__builtin_inff()) {
+                uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+                if (slot < NMAX)
+                    sm.u.cb.keys[slot] = sorted ? key64(cd[g].s, cd[g].idx)
+                                                : (((uint64_t)(~cd[g].idx) << 32) | ord32(cd[g].s));
+            }
         }
     }
     __syncthreads();
     const int N = (int)sm.misc[MISC_N];
+    BFI_TRACE(a, tb, 2);
+    if (a.trace && tid == 0) a.trace[tb + 6] = ((uint64_t)tot << 32) | (uint32_t)N;
     if (N > NMAX) return false;
+    if (N <= WAVE) {
+        combine_wave(a, sm, C, N, sorted, M, S, rawmax);
+        return true;
+    }
     int n2 = 64;
     while (n2 < N) n2 <<= 1;
     for (int j = N + tid; j < n2; j += BLOCK) sm.u.cb.keys[j] = 0ull;
     __syncthreads();
     bitonic_sort_desc(sm.u.cb.keys, n2);
+    BFI_TRACE(a, tb, 3);
     // probabilities of the sorted positions: p = expf(s - M) / S (sample.rs:383, 388)
     for (int j = tid; j < N; j += BLOCK) {
         uint64_t k = sm.u.cb.keys[j];
@@ -610,6 +816,7 @@ __device__ __forceinline__ bool combine_bounded(const KArgs& a, Smem& sm, const 
         if (tid == 0) a.t_listed[C.row] = (int32_t)(tc < a.t_cap ? tc : a.t_cap);
     }
 
+    BFI_TRACE(a, tb, 4);
     const double sum = list_sum(sm, nl, wk);
     if (!C.judged) {  // draw (sample.rs:312-323)
         double r = (double)C.u * sum;
@@ -673,7 +880,7 @@ __device__ __forceinline__ uint32_t scan_chunk_index_order(const KArgs& a, Smem&
     constexpr int EPV = Elem<BF16>::EPV;
     constexpr uint32_t TILE = (uint32_t)BLOCK * VEC * EPV;
     const int tid = threadIdx.x;
-    if (C.pen_on) build_chunk_pen(sm, C, c0, c1);
+    if (C.pen_on) build_chunk_pen(sm, C, c0, c1, hist_prefetch(C));
     float x[VEC][EPV];
     double tsum = 0.0;
     for (uint32_t t0 = c0; t0 < c1; t0 += TILE) {
@@ -738,7 +945,7 @@ __device__ __forceinline__ float element_s(const KArgs& a, Smem& sm, const RowCt
         c = block_sum_u(c, sm.ru);
         if (c) x = penalize(x, c, C.pen);
     }
-    return C.greedy ? x : x / C.T;
+    return C.greedy ? x : div_T(x, C);
 }
 
 template <bool BF16, int VEC>
@@ -902,11 +1109,19 @@ __device__ __forceinline__ Sel radix_select(const KArgs& a, Smem& sm, const RowC
 #pragma unroll
         for (int i = 0; i < BPT; i++) {
             uint32_t o = (uint32_t)tid * BPT + i;
-            bool ok = kind == 0 ? (before_cnt + pc + lc[i] > target) : (before_mass + pm + lm[i] >= target);
+            const uint32_t bc = o < nb ? sm.u.hs.cnt[nb - 1 - o] : 0u;
+            bool ok = kind == 0 ? (before_cnt + pc + lc[i] > target)
+                                : (bc > 0 && before_mass + pm + lm[i] >= target);
             if (hit == 0xFFFFFFFFu && o < nb && ok) hit = o;
         }
         hit = block_min_u(hit, sm.ru);
-        if (hit == 0xFFFFFFFFu) hit = nb - 1;  // target beyond the total: last bucket
+        if (hit == 0xFFFFFFFFu) {  // target beyond the total: the last non-empty bucket
+            uint32_t l = 0;
+            for (uint32_t o = tid; o < nb; o += BLOCK)
+                if (sm.u.hs.cnt[nb - 1 - o] > 0) l = max(l, o + 1);
+            l = (uint32_t)block_max_u64(l, sm.r64);
+            hit = l ? l - 1 : nb - 1;
+        }
         // counts/mass above the chosen bucket
         if ((uint32_t)tid == hit / BPT) {
             const int i = (int)(hit % BPT);
@@ -1150,7 +1365,7 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
 // ---- the kernel ------------------------------------------------------------------------
 
 template <bool BF16, int VEC>
-__global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
+__global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
     constexpr int EPV = Elem<BF16>::EPV;
     __shared__ StreamSmem sm;
     const int tid = threadIdx.x;
@@ -1162,6 +1377,8 @@ __global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
     const uint32_t logical = xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot;
     const int row = (int)(logical / (uint32_t)a.n_chunks);
     const int chunk = (int)(logical % (uint32_t)a.n_chunks);
+    const int64_t tb = (int64_t)logical * 8;
+    BFI_TRACE(a, tb, 0);
     if (row >= a.n_rows) return;
     const RowCtx C = make_ctx(a, row);
     if (!C.active) return;
@@ -1171,9 +1388,11 @@ __global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
     const uint32_t c1 = min(c0 + (uint32_t)a.chunk, V);
 
     // ---- stream phase
+    const HistPre hp = hist_prefetch(C);
     float x[VEC][EPV];
     load_tile<BF16, VEC>(a, row, c0, c1, x);
-    if (C.pen_on) build_chunk_pen(sm, C, c0, c1);
+    if (C.pen_on) build_chunk_pen(sm, C, c0, c1, hp);
+    BFI_TRACE(a, tb, 1);
     const bool track_raw = !C.greedy && C.min_p > 1.0f;
     ArgMax raw{-__builtin_inff(), 0xFFFFFFFFu};
     PenSrc S0{false, c0, nullptr, nullptr, nullptr};
@@ -1182,6 +1401,13 @@ __global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
     else
         transform_tile<BF16, VEC, false>(sm, C, S0, c0, c1, x);
     if (track_raw) raw = block_argmax(raw, sm.rf, sm.ru);
+    if (a.trace) {  // force the transform to complete before the stamp
+        float t = 0.0f;
+#pragma unroll
+        for (int q = 0; q < VEC; q++) t += x[q][0];
+        if (t == 12345.678f) a.trace[tb + 7] = 1;
+    }
+    BFI_TRACE(a, tb, 2);
 
     ChunkPart part;
     part.pad = 0;
@@ -1207,18 +1433,33 @@ __global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
 #pragma unroll
             for (int e = 0; e < EPV; e++) lm = fmaxf(lm, x[q][e]);
         const float mc = block_max(lm, sm.rf);
+        BFI_TRACE(a, tb, 3);
+        part.m = mc;
+        part.arg = 0;
+        const bool kb = C.kmode && C.k <= CAND_CAP;
+        const float margin = 1e-4f + 1e-5f * fabsf(mc);
+        // min-p bound of this chunk: p >= min_p * max p needs s >= max_s + ln(min_p)
+        float th = __builtin_inff();
+        if (C.mmode && mc > -__builtin_inff()) {
+            const float lmp = logf(C.min_p);
+            th = mc + lmp - (margin + 1e-5f * fabsf(lmp));
+        }
+        // one pass: sum of exp(s - max) and the candidate count at th
         float ls = 0.0f;
+        uint32_t lc = 0;
         if (mc > -__builtin_inff()) {
 #pragma unroll
             for (int q = 0; q < VEC; q++)
 #pragma unroll
-                for (int e = 0; e < EPV; e++) ls += __expf(x[q][e] - mc);
+                for (int e = 0; e < EPV; e++) {
+                    const float v = x[q][e];
+                    ls += __expf(v - mc);
+                    lc += (v >= th) ? 1u : 0u;
+                }
         }
-        part.m = mc;
-        part.sum = block_sum(ls, sm.rf);
-        part.arg = 0;
-        // candidate bound (top-k and/or min-p)
-        const bool kb = C.kmode && C.k <= CAND_CAP;
+        uint32_t cnt;
+        part.sum = block_sum_fu(ls, lc, cnt, sm.rf, sm.ru);
+        BFI_TRACE(a, tb, 4);
         if (!(mc > -__builtin_inff())) {
             part.ncand = 0;
             part.theta = -__builtin_inff();
@@ -1226,13 +1467,9 @@ __global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
             part.ncand = NCAND_UNBOUNDED;
             part.theta = __builtin_inff();
         } else {
-            const float margin = 1e-4f + 1e-5f * fabsf(mc);
-            float th = -__builtin_inff();
-            uint32_t cnt = 0xFFFFFFFFu;
-            if (C.mmode) {
-                const float lmp = logf(C.min_p);
-                th = mc + lmp - (margin + 1e-5f * fabsf(lmp));
-                cnt = block_sum_u(tile_count_ge<BF16, VEC>(x, th), sm.ru);
+            if (!C.mmode) {
+                th = -__builtin_inff();
+                cnt = 0xFFFFFFFFu;
             }
             if (kb && cnt > (uint32_t)CAND_CAP) {
                 // smallest power-of-two distance below the chunk max holding k elements,
@@ -1251,7 +1488,8 @@ __global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
                     tk = -__builtin_inff();
                 } else {
                     float hi = d;
-                    for (int j = 0; j < 12 && c > (uint32_t)CAND_CAP; j++) {
+                    const uint32_t want = max(2u * (uint32_t)C.k, 64u);  // a tight bound keeps the gather small
+                    for (int j = 0; j < 12 && c > want; j++) {
                         float mid = 0.5f * (lo + hi);
                         uint32_t cm = block_sum_u(tile_count_ge<BF16, VEC>(x, mc - mid), sm.ru);
                         if (cm >= (uint32_t)C.k) {
@@ -1263,7 +1501,7 @@ __global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
                     }
                     tk = mc - hi - margin;
                 }
-                th = fmaxf(th, tk);
+                th = C.mmode ? fmaxf(th, tk) : tk;
                 cnt = block_sum_u(tile_count_ge<BF16, VEC>(x, th), sm.ru);
             }
             part.theta = th;
@@ -1273,22 +1511,25 @@ __global__ __launch_bounds__(BLOCK) void k_stream(KArgs a) {
                 part.ncand = cnt;
                 uint32_t my = tile_count_ge<BF16, VEC>(x, th), tot;
                 uint32_t o = block_excl_scan<uint32_t>(my, sm.ru, tot);
-                Cand* dst = a.cands + ((int64_t)row * a.n_chunks + chunk) * CAND_CAP;
+                if (my) {
+                    Cand* dst = a.cands + ((int64_t)row * a.n_chunks + chunk) * CAND_CAP;
 #pragma unroll
-                for (int q = 0; q < VEC; q++)
+                    for (int q = 0; q < VEC; q++)
 #pragma unroll
-                    for (int e = 0; e < EPV; e++) {
-                        float s = x[q][e];
-                        if (s >= th && s > -__builtin_inff()) {
-                            dst[o].idx = c0 + (uint32_t)(q * BLOCK + tid) * EPV + e;
-                            dst[o].s = s;
-                            o++;
+                        for (int e = 0; e < EPV; e++) {
+                            float v = x[q][e];
+                            if (v >= th && v > -__builtin_inff()) {
+                                dst[o].idx = c0 + (uint32_t)(q * BLOCK + tid) * EPV + e;
+                                dst[o].s = v;
+                                o++;
+                            }
                         }
-                    }
+                }
             }
         }
     }
     if (tid == 0) a.parts[(int64_t)row * a.n_chunks + chunk] = part;
+    BFI_TRACE(a, tb, 5);
 }
 
 // ---- select kernel: one workgroup per row ----------------------------------------------
@@ -1302,6 +1543,8 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
     const uint32_t G = gridDim.x, bid = blockIdx.x;
     const uint32_t q8 = G / 8, r8 = G % 8, xcd = bid % 8, slot = bid / 8;
     const int row = (int)(xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot);
+    const int64_t tb = ((int64_t)a.n_rows * a.n_chunks + row) * 8;
+    BFI_TRACE(a, tb, 0);
     if (row >= a.n_rows) return;
     const RowCtx C = make_ctx(a, row);
     if (!C.active) return;
@@ -1364,6 +1607,7 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
         a.t_stats[row * 4 + 1] = S;
     }
 
+    BFI_TRACE(a, tb, 1);
     uint32_t flags = 0;  // 1 = some chunk unbounded/overflowed
     if (tid < nc && (mine.ncand == NCAND_UNBOUNDED || mine.ncand == NCAND_OVERFLOW)) flags = 1;
     flags = block_sum_u(flags, sm.ru);
@@ -1374,7 +1618,10 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
     }
     if (flags == 0) {
         if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 1.0f;
-        if (combine_bounded(a, sm, C, mine, M, S, rawmax)) return;
+        if (combine_bounded(a, sm, C, mine, M, S, rawmax, tb)) {
+            BFI_TRACE(a, tb, 7);
+            return;
+        }
     }
     if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 3.0f;
     combine_radix<BF16, VEC>(a, sm, C, M, S, rawmax);

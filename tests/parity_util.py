@@ -41,6 +41,20 @@ def top_p_band(s, top_p, lens):
     return bool(np.any(np.abs(cum[lo:hi] - top_p) <= BAND))
 
 
+def band_draw(s, kept_len, u):
+    """Tokens the reference draw returns at u' in [u - 1e-6, u + 1e-6] over the first
+    kept_len elements of the float64 order (used when the kept length legitimately differs
+    at a top-p boundary)."""
+    pr = exact_probs(s)
+    order = np.argsort(-pr, kind="stable")[:kept_len]
+    cum = np.cumsum(pr[order])
+    toks = set()
+    for uu in u_grid(u):
+        j = int(np.searchsorted(cum, uu * cum[-1], side="left"))
+        toks.add(int(order[min(j, len(order) - 1)]))
+    return toks if len(toks) == 1 else toks | {None}
+
+
 def compare_target(cfg, gpu, orc, logits_f32=None, check_list=True):
     """gpu/orc: dicts of numpy arrays from target_rows. Returns (problems, stats)."""
     B = cfg["B"]
@@ -91,6 +105,8 @@ def compare_target(cfg, gpu, orc, logits_f32=None, check_list=True):
             hist = cfg["hist"][cfg["hist_off"][b]:cfg["hist_off"][b + 1]]
             mask = None if cfg["mask"] is None else cfg["mask"][b]
             if x is not None and any(O.sample(x, hist, p, mask, uu) == tok_g for uu in u_grid(cfg["u"][b])):
+                stats["u_exempt"] += 1
+            elif band and band_draw(orc["s"][b], kl_g, cfg["u"][b]) == {tok_g}:
                 stats["u_exempt"] += 1
             else:
                 problems.append(f"row {b}: token gpu={tok_g} oracle={tok_o} u={cfg['u'][b]} params={p}")
