@@ -1,0 +1,218 @@
+// smp_common.h — what both sampling kernels share: the per-row context (parameters,
+// history view, mask), the 16-byte tile loader and an element's value (mask, penalties,
+// / T) as sample.rs:331-375 computes it.
+#pragma once
+#include "smp_device.h"
+
+namespace bfi {
+
+enum { MISC_LAST = 0, MISC_N = 1, MISC_NDIST = 2, MISC_OVF = 3, MISC_HN = 7 };
+
+// ---- per-row context -------------------------------------------------------------------
+
+struct RowCtx {
+    int row, seq, ri, dl;
+    bool active, verify, judged;
+    uint32_t draft;
+    float u, u2;
+    float T, rT, top_p, min_p;
+    bool fast_div;  // T in [2^-20, 2^20]: FMA-corrected reciprocal division is exact
+    int32_t k;
+    bool greedy, kmode, pmode, mmode;
+    Pen pen;
+    bool pen_on;
+    HistView h;
+    const uint32_t* mrow;
+    const char* lrow;
+};
+
+__device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
+    RowCtx C;
+    C.row = row;
+    C.verify = a.rows_per_seq > 0;
+    if (C.verify) {
+        int rps = a.rows_per_seq;
+        C.seq = row / rps;
+        C.ri = row % rps;
+        int dl = a.draft_len[C.seq];
+        dl = dl < 0 ? 0 : (dl > rps - 1 ? rps - 1 : dl);
+        C.dl = dl;
+        C.active = C.ri <= dl;
+        C.judged = C.ri < dl;
+        const int64_t dbase = (int64_t)C.seq * (rps - 1);
+        C.draft = C.judged ? a.drafts[dbase + C.ri] : 0u;
+        if (C.judged) {
+            C.u = a.u_pairs[(dbase + C.ri) * 2];
+            C.u2 = a.u_pairs[(dbase + C.ri) * 2 + 1];
+        } else {
+            C.u = a.u_bonus[C.seq];
+            C.u2 = 0.0f;
+        }
+        C.h.extra = a.drafts + dbase;
+        C.h.nextra = C.ri;
+    } else {
+        C.seq = row;
+        C.ri = 0;
+        C.dl = 0;
+        C.active = true;
+        C.judged = false;
+        C.draft = 0;
+        C.u = a.u ? a.u[row] : 0.0f;
+        C.u2 = 0.0f;
+        C.h.extra = nullptr;
+        C.h.nextra = 0;
+    }
+    const bfi_smp_row_params P = a.params[C.seq];
+    if (a.hist_off) {
+        int64_t o0 = a.hist_off[C.seq], o1 = a.hist_off[C.seq + 1];
+        C.h.base = a.hist + o0;
+        C.h.nbase = o1 > o0 ? o1 - o0 : 0;
+    } else {
+        C.h.base = nullptr;
+        C.h.nbase = 0;
+    }
+    const int64_t H = C.h.size();
+    C.T = P.temperature;
+    C.rT = 1.0f / P.temperature;  // IEEE, once per row
+    C.fast_div = P.temperature >= 0x1p-20f && P.temperature <= 0x1p20f;
+    C.top_p = P.top_p;
+    C.min_p = P.min_p;
+    C.k = P.top_k;
+    C.greedy = !(P.temperature > 0.0f);                    // sample.rs:369
+    C.kmode = P.top_k > 0 && P.top_k < a.V;                // sample.rs:392
+    C.pmode = P.top_p < 1.0f;                              // sample.rs:397
+    C.mmode = P.min_p > 0.0f;                              // sample.rs:411
+    C.pen.rp = P.repeat_penalty;
+    C.pen.pp = P.presence_penalty;
+    C.pen.fp = P.frequency_penalty;
+    C.pen.rep_on = fabsf(P.repeat_penalty - 1.0f) > F32_EPS && H > 0;  // sample.rs:346
+    C.pen.pres_on = P.presence_penalty != 0.0f && H > 0;               // sample.rs:360
+    C.pen.freq_on = P.frequency_penalty != 0.0f && H > 0;
+    C.pen_on = C.pen.rep_on || C.pen.pres_on || C.pen.freq_on;
+    C.mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
+    const int esz = 4;  // overridden by the loader for bf16
+    (void)esz;
+    C.lrow = (const char*)a.logits;
+    return C;
+}
+
+// ---- chunk loader ----------------------------------------------------------------------
+
+template <bool BF16>
+struct Elem;
+template <>
+struct Elem<false> {
+    static constexpr int EPV = 4;
+    typedef float T;
+    __device__ __forceinline__ static float cvt(T v) { return v; }
+};
+template <>
+struct Elem<true> {
+    static constexpr int EPV = 8;
+    typedef uint16_t T;
+    __device__ __forceinline__ static float cvt(T v) { return __uint_as_float((uint32_t)v << 16); }
+};
+
+// Loads the elements thread `tid` owns in [c0, c1): vector q covers ids
+// c0 + (q*BLOCK + tid)*EPV + [0, EPV). Out-of-range elements read as -inf. A full, aligned
+// tile takes only unconditional 16-byte loads, so all VEC loads are in flight together.
+template <bool BF16, int VEC>
+__device__ __forceinline__ void unpack16(const uint4 w, float (&v)[Elem<BF16>::EPV]) {
+    if (!BF16) {
+        v[0] = __uint_as_float(w.x);
+        v[1] = __uint_as_float(w.y);
+        v[2] = __uint_as_float(w.z);
+        v[3] = __uint_as_float(w.w);
+    } else {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[2 * e] = __uint_as_float(ww[e] << 16);
+            v[2 * e + 1] = __uint_as_float(ww[e] & 0xFFFF0000u);
+        }
+    }
+}
+
+template <bool BF16, int VEC>
+__device__ __forceinline__ void load_tile(const KArgs& a, int row, uint32_t c0, uint32_t c1,
+                                          float (&x)[VEC][Elem<BF16>::EPV]) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    typedef typename Elem<BF16>::T T;
+    const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
+    const int tid = threadIdx.x;
+    if (a.vec_ok && c1 - c0 == (uint32_t)(BLOCK * VEC * EPV)) {
+        uint4 w[VEC];
+#pragma unroll
+        for (int q = 0; q < VEC; q++) w[q] = *(const uint4*)(base + c0 + (uint32_t)(q * BLOCK + tid) * EPV);
+#pragma unroll
+        for (int q = 0; q < VEC; q++) unpack16<BF16, VEC>(w[q], x[q]);
+        return;
+    }
+#pragma unroll
+    for (int q = 0; q < VEC; q++) {
+        const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
+        if (a.vec_ok && id0 + EPV <= c1) {
+            unpack16<BF16, VEC>(*(const uint4*)(base + id0), x[q]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPV; e++)
+                x[q][e] = (id0 + e < c1) ? Elem<BF16>::cvt(base[id0 + e]) : -__builtin_inff();
+        }
+    }
+}
+
+// x / T rounded like IEEE division (sample.rs:373-375). With r = RN(1/T), q = RN(x*r) is
+// within one ulp of x/T, e = x - q*T is exact under FMA, and RN(q + e*r) is the correctly
+// rounded quotient while no step underflows or overflows (Markstein's correction). This was
+// checked bit-exhaustively against IEEE division over all f32 x with |x| in [2^-100, 2^100]
+// for temperatures across [2^-20, 2^20]. Zeros give +-0 and infinities/NaN pass through (e
+// is NaN there, and q is already the quotient). `div_ok` says whether x is in the checked
+// range; other values take IEEE division.
+__device__ __forceinline__ float div_T_fast(float x, const RowCtx& C) {
+    const float q = x * C.rT;
+    const float e = __builtin_fmaf(-q, C.T, x);
+    const float s = __builtin_fmaf(e, C.rT, q);
+    return e != e ? q : s;
+}
+__device__ __forceinline__ bool div_ok(float x) {
+    const uint32_t a = __float_as_uint(x) & 0x7FFFFFFFu;
+    // bad: nonzero below 2^-100, or finite at/above 2^100
+    return !((a - 1u < 0x0D7FFFFFu) || (a - 0x71800000u < 0x0E000000u));
+}
+__device__ __forceinline__ float div_T(float x, const RowCtx& C) {
+    return (C.fast_div && div_ok(x)) ? div_T_fast(x, C) : x / C.T;
+}
+
+// Value of one logit as the streaming pass sees it: masked (sample.rs:331-337), then / T
+// unless greedy. Penalties are not applied here; the select kernel corrects the few
+// history ids afterwards. Exact for |x| in [2^-100, 2^100] (see div_T_fast).
+__device__ __forceinline__ float raw_value(const RowCtx& C, float x, bool allowed) {
+    if (!allowed) return -__builtin_inff();
+    return C.greedy ? x : div_T(x, C);
+}
+// Value with the penalties (sample.rs:345-375): mask, repeat, presence, frequency, / T.
+__device__ __forceinline__ float pen_value(const RowCtx& C, float x, bool allowed, uint32_t count) {
+    float v = allowed ? x : -__builtin_inff();
+    v = penalize(v, count, C.pen);
+    return C.greedy ? v : div_T(v, C);
+}
+
+// ---- small helpers ---------------------------------------------------------------------
+
+template <bool BF16, int VEC>
+__device__ __forceinline__ uint32_t tile_count_ge(const float (&x)[VEC][Elem<BF16>::EPV], float th) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    uint32_t c = 0;
+#pragma unroll
+    for (int q = 0; q < VEC; q++)
+#pragma unroll
+        for (int e = 0; e < EPV; e++) c += (x[q][e] >= th && x[q][e] > -__builtin_inff()) ? 1u : 0u;
+    return c;
+}
+
+__device__ __forceinline__ uint64_t efix_of(float s, float M, double scale) {
+    float e = expf(s - M);
+    return (uint64_t)((double)e * scale);
+}
+
+}  // namespace bfi

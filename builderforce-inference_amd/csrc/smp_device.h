@@ -21,20 +21,26 @@ constexpr int NMAX = 2048;             // combine sort capacity (power of two)
 constexpr int NBUCKET = 1024;          // radix buckets (10-bit digits) of the fallback select
 constexpr int DCAP = 1024;             // distinct history ids counted per chunk in LDS
 constexpr int GDCAP = 4096;            // distinct history ids counted per row (global scratch)
+constexpr int HSLOTS_LOG2 = 11;
+constexpr int HSLOTS = 1 << HSLOTS_LOG2;  // LDS history hash slots (select kernel)
+constexpr int HMAX = 1536;             // distinct history ids the hash takes (75% load)
+constexpr uint32_t HEMPTY = 0xFFFFFFFFu;
 constexpr uint32_t NCAND_UNBOUNDED = 0xFFFFFFFFu;  // row has no top-k / min-p bound
 constexpr uint32_t NCAND_OVERFLOW = 0xFFFFFFFEu;   // chunk had more than CAND_CAP candidates
 constexpr float F32_EPS = 1.1920928955078125e-07f;  // f32::EPSILON
 
-// Per (row, chunk) result of the stream phase.
+// Per (row, chunk) result of the streaming pass, over un-penalized values s = masked/T
+// (greedy: masked logits).
 struct ChunkPart {
-    float m;          // max of s = penalized/T (or of penalized logits when greedy)
-    float sum;        // sum over the chunk of exp(s - m)
+    float m;          // max of s
     uint32_t arg;     // greedy: first index attaining m
+    double sum;       // sum of the f32 terms __expf(s - m), accumulated in f64
     uint32_t ncand;   // candidates written, or NCAND_UNBOUNDED / NCAND_OVERFLOW
     float theta;      // every element of the chunk with finite s >= theta was written
     float raw_m;      // max of masked, un-penalized logits (only when min_p > 1)
     uint32_t raw_arg; // its first index
     uint32_t pad;
+    uint32_t pad2;
 };
 
 struct Cand {
@@ -103,6 +109,9 @@ __device__ __forceinline__ uint32_t lds_add(uint32_t* p, uint32_t v) {
 }
 __device__ __forceinline__ uint32_t lds_or(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_or((BFI_LDS uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint32_t lds_max(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_max((BFI_LDS uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 __device__ __forceinline__ uint64_t lds_add64(uint64_t* p, uint64_t v) {
     return __hip_atomic_fetch_add((BFI_LDS uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -243,6 +252,26 @@ __device__ __forceinline__ uint32_t block_sum_u(uint32_t v, uint32_t* scr) {
 #pragma unroll
     for (int w = 0; w < NWAVE; w++) r += scr[w];
     __syncthreads();
+    return r;
+}
+// Sum of a double and of a count in one pair of barriers.
+__device__ __forceinline__ double block_sum_du(double v, uint32_t c, uint32_t& csum, double* scrd, uint32_t* scru) {
+    v = wave_sum_d(v);
+    c = wave_sum_u(c);
+    if (lane_id() == 0) {
+        scrd[wave_id()] = v;
+        scru[wave_id()] = c;
+    }
+    __syncthreads();
+    double r = scrd[0];
+    uint32_t rc = scru[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) {
+        r += scrd[w];
+        rc += scru[w];
+    }
+    __syncthreads();
+    csum = rc;
     return r;
 }
 // Sum of a float and of a count in one pair of barriers.

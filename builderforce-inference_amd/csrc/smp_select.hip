@@ -1,0 +1,1565 @@
+// smp_select.hip — the select pass of the gfx950 token sampler: one workgroup per row.
+//
+// It reads the streaming pass's per-chunk results, applies the repetition / presence /
+// frequency penalties (sample.rs:345-368) to the row's history ids as corrections, and
+// finishes the row:
+//   - greedy: argmax (sample.rs:369-371, 429-439);
+//   - bounded candidates (top-k <= 2048 or min-p > 0): gather, one sort in LDS, then
+//     top-k / top-p / min-p and the draw by f64 scans (sample.rs:392-426, 312-323);
+//   - rows without top-k/top-p: the draw in index order from per-chunk masses plus one
+//     chunk re-read;
+//   - unbounded rows (top-p without top-k/min-p, or candidate overflow): radix select over
+//     the row (10-bit digits of a 64-bit (value, index) key, with counts and fixed-point
+//     masses), re-reading the row.
+// Spec verify applies judge() (spec.rs:79-97) to each row's target; the last row of a
+// sequence to finish computes the accepted prefix.
+#include "smp_common.h"
+
+namespace bfi {
+
+// ---- shared memory ---------------------------------------------------------------------
+
+struct __align__(16) Smem {
+    union {
+        struct {
+            uint64_t keys[NMAX];
+            float p[NMAX];
+        } cb;
+        struct {
+            uint64_t mass[NBUCKET];
+            uint32_t cnt[NBUCKET];
+        } hs;
+    } u;
+    // history set of the row (ids < V): open addressing, linear probing
+    uint32_t hkey[HSLOTS];
+    uint32_t hcnt[HSLOTS];
+    float hraw[HSLOTS];        // value the streaming pass used (masked, /T)
+    float hpen[HSLOTS];        // penalized value (sample.rs:345-375)
+    // per-chunk tables (index = chunk)
+    float cm[BLOCK];           // max over the chunk's non-history elements
+    uint32_t carg[BLOCK];      // its first index (greedy)
+    double csum[BLOCK];        // sum of exp(s - cm) over them, or a chunk mass
+    uint32_t cflag[BLOCK];     // ord32 of the largest history value, then the dirty flag
+    uint64_t craw[BLOCK];      // fixed-point streaming-pass terms of the chunk's history ids
+    uint64_t cpen[BLOCK];      // fixed-point penalized terms exp(s - M) of its history ids
+    uint32_t cpre[BLOCK + 1];  // per-chunk candidate prefix (combine)
+    float rf[NWAVE];
+    float rf2[NWAVE];
+    uint32_t ru[NWAVE];
+    uint32_t ru2[NWAVE];
+    double rd[NWAVE];
+    uint64_t r64[NWAVE];
+    uint64_t r64b[NWAVE];
+    uint32_t misc[8];
+};
+
+// ---- history structures ----------------------------------------------------------------
+
+// Row-wide history bitmap + dense counts in global scratch (fallback passes over the row).
+__device__ __forceinline__ void build_row_pen(const KArgs& a, Smem& sm, const RowCtx& C) {
+    if (!C.pen_on) return;
+    const int tid = threadIdx.x;
+    const int nw = a.bm_words;
+    uint32_t* bm = a.row_pen + (int64_t)C.row * (2 * nw + GDCAP);
+    uint32_t* pre = bm + nw;
+    uint32_t* cnt = pre + nw;
+    for (int w = tid; w < nw; w += BLOCK) bm[w] = 0;
+    if (C.pen.freq_on)
+        for (int w = tid; w < GDCAP; w += BLOCK) cnt[w] = 0;
+    __threadfence();
+    __syncthreads();
+    const int64_t H = C.h.size();
+    for (int64_t j = tid; j < H; j += BLOCK) {
+        uint32_t id = C.h.at(j);
+        if (id < (uint32_t)a.V) glb_or(&bm[id >> 5], 1u << (id & 31));
+    }
+    __threadfence();
+    __syncthreads();
+    if (C.pen.freq_on) {
+        // popcount prefix over nw words: each thread a contiguous run
+        const int per = (nw + BLOCK - 1) / BLOCK;
+        const int w0 = tid * per;
+        uint32_t s = 0;
+        for (int w = w0; w < w0 + per && w < nw; w++) s += __popc(bm[w]);
+        uint32_t tot;
+        uint32_t run = block_excl_scan<uint32_t>(s, sm.ru, tot);
+        for (int w = w0; w < w0 + per && w < nw; w++) {
+            pre[w] = run;
+            run += __popc(bm[w]);
+        }
+        if (tid == 0) sm.misc[MISC_NDIST] = tot;
+        __threadfence();
+        __syncthreads();
+        if (tot <= GDCAP) {
+            for (int64_t j = tid; j < H; j += BLOCK) {
+                uint32_t id = C.h.at(j);
+                if (id < (uint32_t)a.V) glb_add(&cnt[dense_rank(pre[id >> 5], bm[id >> 5], id & 31)], 1u);
+            }
+        }
+        __threadfence();
+        __syncthreads();
+    }
+}
+
+// ---- history set (select kernel): ids < V with occurrence counts ------------------------
+
+__device__ __forceinline__ uint32_t hslot0(uint32_t id) { return (id * 2654435761u) >> (32 - HSLOTS_LOG2); }
+
+__device__ __forceinline__ uint32_t lds_cas(uint32_t* p, uint32_t expected, uint32_t desired) {
+    __hip_atomic_compare_exchange_strong((BFI_LDS uint32_t*)p, &expected, desired, __ATOMIC_RELAXED,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return expected;  // the previous value
+}
+
+// Slot of `id`, or -1 when absent.
+__device__ __forceinline__ int hist_find(const Smem& sm, uint32_t id) {
+    uint32_t s = hslot0(id);
+    for (int probe = 0; probe < HSLOTS; probe++) {
+        const uint32_t k = sm.hkey[s];
+        if (k == id) return (int)s;
+        if (k == HEMPTY) return -1;
+        s = (s + 1) & (HSLOTS - 1);
+    }
+    return -1;
+}
+
+// The reference's `HashSet(prev)` (sample.rs:347, 361) plus multiset counts (frequency
+// extension). Returns false when the row has more than HMAX distinct ids.
+__device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCtx& C) {
+    const int tid = threadIdx.x;
+    for (int k = tid; k < HSLOTS; k += BLOCK) {
+        sm.hkey[k] = HEMPTY;
+        sm.hcnt[k] = 0;
+    }
+    if (tid == 0) sm.misc[MISC_HN] = 0;
+    __syncthreads();
+    if (C.pen_on) {
+        const int64_t H = C.h.size();
+        for (int64_t j = tid; j < H; j += BLOCK) {
+            const uint32_t id = C.h.at(j);
+            if (id >= (uint32_t)a.V) continue;
+            uint32_t k = hslot0(id);
+            for (int probe = 0; probe < HSLOTS; probe++) {
+                const uint32_t prev = lds_cas(&sm.hkey[k], HEMPTY, id);
+                if (prev == HEMPTY || prev == id) {
+                    if (prev == HEMPTY) lds_add(&sm.misc[MISC_HN], 1u);
+                    lds_add(&sm.hcnt[k], 1u);
+                    break;
+                }
+                k = (k + 1) & (HSLOTS - 1);
+            }
+        }
+    }
+    __syncthreads();
+    return sm.misc[MISC_HN] <= (uint32_t)HMAX;
+}
+
+// Where the penalty membership/counts of an element come from in passes over the row.
+struct PenSrc {
+    bool hash;                  // LDS history hash (else the global row tables)
+    const uint32_t* gbm;        // row tables (global)
+    const uint32_t* gpre;
+    const uint32_t* gcnt;
+};
+
+__device__ __forceinline__ uint32_t pen_bits(const Smem& sm, const PenSrc& S, uint32_t id0, int epv) {
+    const uint32_t em = (1u << epv) - 1u;
+    if (S.hash) {
+        uint32_t b = 0;
+        for (int e = 0; e < epv; e++) b |= (hist_find(sm, id0 + e) >= 0 ? 1u : 0u) << e;
+        return b;
+    }
+    return (S.gbm[id0 >> 5] >> (id0 & 31)) & em;
+}
+__device__ __forceinline__ uint32_t pen_count(const Smem& sm, const PenSrc& S, const RowCtx& C, uint32_t id) {
+    if (!C.pen.freq_on) return 0;
+    if (S.hash) {
+        const int k = hist_find(sm, id);
+        return k >= 0 ? sm.hcnt[k] : 0u;
+    }
+    if (sm.misc[MISC_NDIST] > GDCAP) return C.h.count_scan(id);
+    return S.gcnt[dense_rank(S.gpre[id >> 5], S.gbm[id >> 5], id & 31)];
+}
+
+// In place over one tile of a pass over the row: the streaming value (raw_value) for every
+// element, the penalized value (pen_value) for the history ids.
+template <bool BF16, int VEC>
+__device__ __forceinline__ void transform_tile(const Smem& sm, const RowCtx& C, const PenSrc& S, uint32_t c0,
+                                               uint32_t c1, float (&x)[VEC][Elem<BF16>::EPV]) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    const int tid = threadIdx.x;
+    const uint32_t em = (1u << EPV) - 1u;
+#pragma unroll
+    for (int q = 0; q < VEC; q++) {
+        const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
+        if (id0 >= c1) continue;  // all -inf already
+        const uint32_t mb = C.mrow ? (C.mrow[id0 >> 5] >> (id0 & 31)) & em : em;
+        const uint32_t pb = C.pen_on ? pen_bits(sm, S, id0, EPV) : 0u;
+        if (pb) {  // rare: an id of the history in this vector
+#pragma unroll
+            for (int e = 0; e < EPV; e++)
+                x[q][e] = ((pb >> e) & 1u) ? pen_value(C, x[q][e], (mb >> e) & 1u, pen_count(sm, S, C, id0 + e))
+                                           : raw_value(C, x[q][e], (mb >> e) & 1u);
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPV; e++) x[q][e] = raw_value(C, x[q][e], (mb >> e) & 1u);
+        }
+    }
+}
+
+// One pass over [c0, c1) of the row: f(id, s) for every element, s = its value with the
+// penalties from P; with SKIP_HIST, only for the ids outside the history hash, at their
+// streaming-pass values.
+template <bool BF16, int VEC, bool SKIP_HIST, typename F>
+__device__ __forceinline__ void span_pass(const KArgs& a, const Smem& sm, const RowCtx& C, const PenSrc& P,
+                                          uint32_t c0, uint32_t c1, F f) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    constexpr uint32_t TILE = (uint32_t)BLOCK * VEC * EPV;
+    const uint32_t em = (1u << EPV) - 1u;
+    for (uint32_t t0 = c0; t0 < c1; t0 += TILE) {
+        const uint32_t t1 = min(t0 + TILE, c1);
+        float x[VEC][EPV];
+        load_tile<BF16, VEC>(a, C.row, t0, t1, x);
+        if (!SKIP_HIST) transform_tile<BF16, VEC>(sm, C, P, t0, t1, x);
+#pragma unroll
+        for (int q = 0; q < VEC; q++) {
+            const uint32_t id0 = t0 + (uint32_t)(q * BLOCK + threadIdx.x) * EPV;
+            if (id0 >= t1) continue;
+            uint32_t mb = em;
+            if (SKIP_HIST && C.mrow) mb = (C.mrow[id0 >> 5] >> (id0 & 31)) & em;
+#pragma unroll
+            for (int e = 0; e < EPV; e++) {
+                const uint32_t id = id0 + e;
+                if (id >= t1) continue;
+                if (SKIP_HIST) {
+                    if (C.pen_on && hist_find(sm, id) >= 0) continue;
+                    f(id, raw_value(C, x[q][e], (mb >> e) & 1u));
+                } else {
+                    f(id, x[q][e]);
+                }
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t chunk_lo(const KArgs& a, uint32_t c) { return c * (uint32_t)a.chunk; }
+__device__ __forceinline__ uint32_t chunk_hi(const KArgs& a, uint32_t c) {
+    return min(c * (uint32_t)a.chunk + (uint32_t)a.chunk, (uint32_t)a.V);
+}
+
+// ---- result emission (sample / target / verify) ----------------------------------------
+
+// Stores the row's outcome. For spec verify, `verdict` is 1 = Accept, 0 = Reject(token),
+// and the last row of a sequence to finish resolves the accepted prefix (spec.rs:140-162).
+__device__ __forceinline__ void emit(const KArgs& a, Smem& sm, const RowCtx& C, uint32_t token, uint32_t verdict) {
+    const int tid = threadIdx.x;
+    if (!C.verify) {
+        if (tid == 0) {
+            if (a.out_tok) a.out_tok[C.row] = token;
+        }
+        return;
+    }
+    if (tid == 0) {
+        a.row_res[2 * C.row] = C.judged ? verdict : 2u;
+        a.row_res[2 * C.row + 1] = token;
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t prev = glb_add(&a.seq_ctr[C.seq], 1u);
+        sm.misc[MISC_LAST] = prev == (uint32_t)C.dl;
+    }
+    __syncthreads();
+    if (!sm.misc[MISC_LAST]) return;
+    __threadfence();
+    if (tid == 0) {
+        a.seq_ctr[C.seq] = 0;
+        const int base = C.seq * a.rows_per_seq;
+        int acc = C.dl;
+        for (int i = 0; i < C.dl; i++) {
+            if (__hip_atomic_load(&a.row_res[2 * (base + i)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+                acc = i;
+                break;
+            }
+        }
+        a.out_accepted[C.seq] = acc;
+        a.out_next[C.seq] =
+            __hip_atomic_load(&a.row_res[2 * (base + acc) + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__device__ __forceinline__ void emit_target_token(const KArgs& a, const RowCtx& C, uint32_t tok) {
+    if (threadIdx.x == 0 && a.t_kind) {
+        a.t_kind[C.row] = BFI_SMP_TARGET_TOKEN;
+        a.t_kept[C.row] = 0;
+        a.t_listed[C.row] = 0;
+        if (a.out_tok) a.out_tok[C.row] = tok;
+    }
+}
+
+// Token target (greedy, min-p fallback): judge is exact equality (spec.rs:81-82).
+__device__ __forceinline__ void finish_token(const KArgs& a, Smem& sm, const RowCtx& C, uint32_t tok) {
+    emit_target_token(a, C, tok);
+    if (C.judged)
+        emit(a, sm, C, tok, tok == C.draft ? 1u : 0u);
+    else
+        emit(a, sm, C, tok, 1u);
+}
+
+// ---- f64 scans over a sorted list in LDS (bounded-candidate path) ----------------------
+
+constexpr int PT = NMAX / BLOCK;  // positions per thread
+
+// First position j < n (in list order) with pred(j) and inclusive cum(w) >= target, where
+// w(j) is the weight of position j; UINT32_MAX if none.
+template <typename W, typename P>
+__device__ __forceinline__ uint32_t first_cum_ge(Smem& sm, int n, W w, P pred, double target) {
+    const int tid = threadIdx.x;
+    double loc[PT];
+    double run = 0.0;
+#pragma unroll
+    for (int i = 0; i < PT; i++) {
+        int j = tid * PT + i;
+        run += (j < n) ? w(j) : 0.0;
+        loc[i] = run;
+    }
+    double tot;
+    double pre = block_excl_scan<double>(run, sm.rd, tot);
+    uint32_t best = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < PT; i++) {
+        int j = tid * PT + i;
+        if (best == 0xFFFFFFFFu && j < n && pred(j) && pre + loc[i] >= target) best = (uint32_t)j;
+    }
+    return block_min_u(best, sm.ru);
+}
+
+template <typename W>
+__device__ __forceinline__ double list_sum(Smem& sm, int n, W w) {
+    const int tid = threadIdx.x;
+    double run = 0.0;
+#pragma unroll
+    for (int i = 0; i < PT; i++) {
+        int j = tid * PT + i;
+        run += (j < n) ? w(j) : 0.0;
+    }
+    return block_sum_d(run, sm.rd);
+}
+
+__device__ __forceinline__ void bitonic_sort_desc(uint64_t* k, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < n / 2; i += BLOCK) {
+                int lo = 2 * i - (i & (stride - 1));
+                int hi = lo + stride;
+                bool desc = (lo & size) == 0;
+                uint64_t x = k[lo], y = k[hi];
+                if ((x < y) == desc) {
+                    k[lo] = y;
+                    k[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ---- combine: bounded candidates -------------------------------------------------------
+//
+// The list in sm.u.cb.keys holds every element whose (penalized) value is >= th: the
+// non-history elements from the chunks' candidates (complete above each chunk's bound) and
+// the history ids at their penalized values. The kept set is a prefix of its sorted order
+// when the cut falls inside it; `exhaustive` = every finite element is listed, and
+// `minp_complete` = every element passing min-p is listed.
+
+constexpr int64_t L_UNKNOWN = INT64_MAX;  // lies beyond the listed prefix
+
+// Resolves L = min(L_k, L_p, L_m) (sample.rs:392-414) from the per-position flags; returns
+// false when the cut lies beyond the listed prefix.
+__device__ __forceinline__ bool resolve_L(int64_t Lk, int64_t Lp, int64_t Lm, int N, bool exhaustive, int64_t& L) {
+    L = min(Lk, min(Lp, Lm));
+    return L != L_UNKNOWN && (L <= N || exhaustive);
+}
+
+// N <= 64 candidates: wave 0 does everything in registers with shuffles and ballots; the
+// other waves wait for the result. Returns false when the list does not decide the cut.
+__device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const RowCtx& C, int N, bool sorted, float M,
+                                             float S, ArgMax rawmax, bool exhaustive, bool minp_complete) {
+    enum { R_TOK = 0, R_VERDICT = 1, R_KIND = 2 };  // R_KIND: 0 weights, 1 token target, 2 undecided
+    if (wave_id() == 0) {
+        const int lane = lane_id();
+        const bool valid = lane < N;
+        uint64_t key = valid ? sm.u.cb.keys[lane] : 0ull;
+        key = wave_sort_desc(key);
+        const float s = sorted ? key_s(key) : unord32((uint32_t)key);
+        const uint32_t idx = sorted ? key_idx(key) : ~(uint32_t)(key >> 32);
+        const float p = valid ? expf(s - M) / S : 0.0f;  // sample.rs:383, 388
+        const int64_t Lk = C.kmode ? C.k : a.V;
+        const int lim = (int)(Lk < N ? Lk : N);
+        int64_t Lp = Lk, Lm = L_UNKNOWN;
+        if (sorted && C.pmode) {  // sample.rs:397-409
+            const double cum = wave_incl_scan_d((double)p);
+            const uint64_t hit = __ballot(lane < lim && cum >= (double)C.top_p);
+            if (hit) Lp = (int64_t)__ffsll((unsigned long long)hit);
+            else if (!(Lk <= N || exhaustive)) Lp = L_UNKNOWN;
+        }
+        float thresh = 0.0f;
+        uint32_t kind = 0, tok = 0, verdict = 1;
+        if (C.mmode) {  // sample.rs:411-414
+            thresh = C.min_p * (1.0f / S);
+            if (sorted) {
+                const int64_t trunc = min(Lk, Lp);
+                const int64_t n_in = trunc < N ? trunc : N;
+                const uint64_t fail = __ballot(lane < n_in && p < thresh);
+                if (fail) Lm = (int64_t)__ffsll((unsigned long long)fail) - 1;
+                else if (trunc <= N) Lm = trunc;
+                else if (minp_complete || exhaustive) Lm = N;
+            } else {
+                const int64_t c = __popcll(__ballot(valid && p >= thresh));
+                if (minp_complete || exhaustive) Lm = c;
+            }
+            if (Lm == 0) {  // sample.rs:415-422
+                kind = 1;
+                tok = rawmax.v > -__builtin_inff() ? rawmax.i : 0u;
+                verdict = C.judged ? (tok == C.draft) : 1u;
+            }
+        }
+        int64_t L = 0;
+        if (kind == 0) {
+            bool ok;
+            if (sorted) {
+                ok = resolve_L(Lk, Lp, C.mmode ? Lm : L_UNKNOWN, N, exhaustive, L);
+            } else {
+                ok = Lm != L_UNKNOWN;
+                L = Lm;
+            }
+            if (!ok) kind = 2;
+        }
+        if (kind == 0) {
+            const int nl = sorted ? (int)(L < N ? L : N) : N;
+            const bool kept = sorted ? lane < nl : (valid && p >= thresh);
+            if (a.t_kind) {
+                const bool listed = kept && p > 0.0f;
+                const uint64_t lm = __ballot(listed);
+                const int o = __popcll(lm & lanes_below());
+                if (listed && o < a.t_cap) {
+                    a.t_ids[(int64_t)C.row * a.t_cap + o] = idx;
+                    a.t_probs[(int64_t)C.row * a.t_cap + o] = p;
+                }
+                if (lane == 0) {
+                    a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
+                    a.t_kept[C.row] = (int32_t)L;
+                    a.t_listed[C.row] = (int32_t)min((int64_t)__popcll(lm), a.t_cap);
+                }
+            }
+            const double w = kept ? (double)p : 0.0;
+            const double cumk = wave_incl_scan_d(w);
+            const double sum = __shfl(cumk, WAVE - 1);
+            if (!C.judged) {  // draw, sample.rs:312-323
+                const double r = (double)C.u * sum;
+                const uint64_t hit = __ballot(kept && cumk >= r);
+                const int j = hit ? __ffsll((unsigned long long)hit) - 1 : 0;
+                tok = __shfl(idx, j);
+            } else {  // judge, spec.rs:83-95
+                const uint64_t dm = __ballot(kept && idx == C.draft);
+                const int pd = dm ? __ffsll((unsigned long long)dm) - 1 : -1;
+                const double p_d = pd >= 0 ? (double)__shfl(p, pd) : 0.0;
+                if (sum > 0.0 && (double)C.u < p_d / sum) {
+                    tok = C.draft;
+                    verdict = 1;
+                } else {
+                    const bool res = kept && lane != pd;
+                    if (__ballot(res && p > 0.0f) == 0) {  // residual empty or all <= 0
+                        tok = C.draft;
+                        verdict = 1;
+                    } else {
+                        const double cum2 = wave_incl_scan_d(res ? (double)p : 0.0);
+                        const double r2 = (double)C.u2 * (sum - p_d);
+                        const uint64_t hit = __ballot(res && cum2 >= r2);
+                        const int j = hit ? __ffsll((unsigned long long)hit) - 1 : 0;
+                        tok = __shfl(idx, j);
+                        verdict = 0;
+                    }
+                }
+            }
+        }
+        if (lane == 0) {
+            sm.misc[4 + R_TOK] = tok;
+            sm.misc[4 + R_VERDICT] = verdict;
+            sm.misc[4 + R_KIND] = kind;
+        }
+    }
+    __syncthreads();
+    const uint32_t tok = sm.misc[4 + R_TOK], verdict = sm.misc[4 + R_VERDICT], kind = sm.misc[4 + R_KIND];
+    __syncthreads();
+    if (kind == 2) return false;
+    if (kind == 1) {
+        finish_token(a, sm, C, tok);
+        return true;
+    }
+    if (a.t_kind && threadIdx.x == 0 && a.out_tok) a.out_tok[C.row] = tok;
+    emit(a, sm, C, tok, verdict);
+    return true;
+}
+
+// Re-reads chunk c: appends its non-history elements with value >= th to the list.
+template <bool BF16, int VEC>
+__device__ __forceinline__ void rescan_collect(const KArgs& a, Smem& sm, const RowCtx& C, uint32_t c, float th,
+                                               bool sorted) {
+    const PenSrc P{true, nullptr, nullptr, nullptr};
+    span_pass<BF16, VEC, true>(a, sm, C, P, chunk_lo(a, c), chunk_hi(a, c), [&](uint32_t id, float v) {
+        if (v >= th && v > -__builtin_inff()) {
+            const uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+            if (slot < NMAX) sm.u.cb.keys[slot] = sorted ? key64(v, id) : (((uint64_t)(~id) << 32) | ord32(v));
+        }
+    });
+}
+
+enum { CB_DONE = 0, CB_RADIX = 1 };
+
+// N in (64, NMAX] candidates: one bitonic sort in LDS, then f64 scans. Returns CB_DONE, or
+// -1 when the list does not decide the cut (nothing has been written then).
+__device__ __forceinline__ int combine_list(const KArgs& a, Smem& sm, const RowCtx& C, int N, bool sorted, float M,
+                                            float S, ArgMax rawmax, bool exhaustive, bool minp_complete,
+                                            int64_t tb) {
+    const int tid = threadIdx.x;
+    int n2 = 64;
+    while (n2 < N) n2 <<= 1;
+    for (int j = N + tid; j < n2; j += BLOCK) sm.u.cb.keys[j] = 0ull;
+    __syncthreads();
+    bitonic_sort_desc(sm.u.cb.keys, n2);
+    BFI_TRACE(a, tb, 3);
+    // probabilities of the sorted positions: p = expf(s - M) / S (sample.rs:383, 388)
+    for (int j = tid; j < N; j += BLOCK) {
+        const uint64_t k = sm.u.cb.keys[j];
+        const float s = sorted ? key_s(k) : unord32((uint32_t)k);
+        sm.u.cb.p[j] = expf(s - M) / S;
+    }
+    __syncthreads();
+    auto idx_at = [&](int j) -> uint32_t {
+        const uint64_t k = sm.u.cb.keys[j];
+        return sorted ? key_idx(k) : ~(uint32_t)(k >> 32);
+    };
+    const float* p = sm.u.cb.p;
+
+    const int64_t Lk = C.kmode ? C.k : a.V;
+    int64_t Lp = Lk, Lm = L_UNKNOWN;
+    const int lim = (int)(Lk < N ? Lk : N);
+    if (sorted && C.pmode) {  // sample.rs:397-409
+        const uint32_t j = first_cum_ge(sm, lim, [&](int i) { return (double)p[i]; }, [](int) { return true; },
+                                        (double)C.top_p);
+        if (j != 0xFFFFFFFFu) Lp = (int64_t)j + 1;
+        else if (!(Lk <= N || exhaustive)) Lp = L_UNKNOWN;
+    }
+    float thresh = 0.0f;
+    if (C.mmode) {  // sample.rs:411-414
+        thresh = C.min_p * (1.0f / S);
+        if (sorted) {
+            const int64_t trunc = min(Lk, Lp);
+            const int n_in = (int)(trunc < N ? trunc : N);
+            const uint32_t j = first_cum_ge(sm, n_in, [&](int i) { return p[i] >= thresh ? 0.0 : 1.0; },
+                                            [](int) { return true; }, 0.5);
+            if (j != 0xFFFFFFFFu) Lm = (int64_t)j;
+            else if (trunc <= N) Lm = trunc;
+            else if (minp_complete || exhaustive) Lm = N;
+        } else {
+            uint32_t c = 0;
+            for (int j = tid; j < N; j += BLOCK) c += p[j] >= thresh;
+            c = block_sum_u(c, sm.ru);
+            if (minp_complete || exhaustive) Lm = c;
+        }
+        if (Lm == 0) {  // sample.rs:415-422: argmax of the masked, un-penalized logits
+            const uint32_t tok = rawmax.v > -__builtin_inff() ? rawmax.i : 0u;
+            finish_token(a, sm, C, tok);
+            return CB_DONE;
+        }
+    }
+    int64_t L;
+    if (sorted) {
+        if (!resolve_L(Lk, Lp, C.mmode ? Lm : L_UNKNOWN, N, exhaustive, L)) return -1;
+    } else {
+        if (Lm == L_UNKNOWN) return -1;
+        L = Lm;
+    }
+    const int nl = sorted ? (int)(L < N ? L : N) : N;  // list positions that can be kept
+    auto kept = [&](int j) -> bool { return sorted ? j < nl : (p[j] >= thresh); };
+    auto wk = [&](int j) -> double { return kept(j) ? (double)p[j] : 0.0; };
+
+    // target introspection: kept entries with p > 0 in draw order
+    if (a.t_kind) {
+        if (tid == 0) {
+            a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
+            a.t_kept[C.row] = (int32_t)L;
+        }
+        uint32_t c = 0;
+        for (int j = tid * PT; j < tid * PT + PT; j++) c += (j < nl && kept(j) && p[j] > 0.0f);
+        uint32_t tc;
+        uint32_t o = block_excl_scan<uint32_t>(c, sm.ru, tc);
+        for (int j = tid * PT; j < tid * PT + PT; j++) {
+            if (j < nl && kept(j) && p[j] > 0.0f) {
+                if ((int64_t)o < a.t_cap) {
+                    a.t_ids[(int64_t)C.row * a.t_cap + o] = idx_at(j);
+                    a.t_probs[(int64_t)C.row * a.t_cap + o] = p[j];
+                }
+                o++;
+            }
+        }
+        if (tid == 0) a.t_listed[C.row] = (int32_t)(tc < a.t_cap ? tc : a.t_cap);
+    }
+
+    BFI_TRACE(a, tb, 4);
+    const double sum = list_sum(sm, nl, wk);
+    if (!C.judged) {  // draw (sample.rs:312-323)
+        const double r = (double)C.u * sum;
+        const uint32_t j = first_cum_ge(sm, nl, wk, kept, r);
+        const uint32_t tok = j == 0xFFFFFFFFu ? 0u : idx_at((int)j);
+        if (a.t_kind && tid == 0 && a.out_tok) a.out_tok[C.row] = tok;
+        emit(a, sm, C, tok, 1u);
+        return CB_DONE;
+    }
+    // judge (spec.rs:83-95)
+    uint32_t pd = 0xFFFFFFFFu;
+    for (int j = tid; j < nl; j += BLOCK)
+        if (kept(j) && idx_at(j) == C.draft) pd = (uint32_t)j;
+    pd = block_min_u(pd, sm.ru);
+    const double p_d = pd == 0xFFFFFFFFu ? 0.0 : (double)p[pd];
+    if (sum > 0.0 && (double)C.u < p_d / sum) {
+        emit(a, sm, C, C.draft, 1u);
+        return CB_DONE;
+    }
+    uint32_t pos = 0;
+    for (int j = tid; j < nl; j += BLOCK) pos += (kept(j) && (uint32_t)j != pd && p[j] > 0.0f);
+    pos = block_sum_u(pos, sm.ru);
+    if (pos == 0) {  // residual empty or all <= 0: Accept (spec.rs:90-93)
+        emit(a, sm, C, C.draft, 1u);
+        return CB_DONE;
+    }
+    auto wr = [&](int j) -> double { return (kept(j) && (uint32_t)j != pd) ? (double)p[j] : 0.0; };
+    const double r2 = (double)C.u2 * (sum - p_d);
+    const uint32_t j = first_cum_ge(sm, nl, wr, [&](int i) { return kept(i) && (uint32_t)i != pd; }, r2);
+    emit(a, sm, C, j == 0xFFFFFFFFu ? 0u : idx_at((int)j), 0u);
+    return CB_DONE;
+}
+
+
+// Bounded rows (top-k <= CAND_CAP or min-p > 0, every chunk within CAND_CAP).
+template <bool BF16, int VEC>
+__device__ __forceinline__ int combine_bounded(const KArgs& a, Smem& sm, const RowCtx& C, const ChunkPart& mine,
+                                               float M, float S, ArgMax rawmax, int64_t tb) {
+    const int tid = threadIdx.x;
+    const int nc = a.n_chunks;
+    const bool sorted = C.kmode || C.pmode;  // else min-p only: index order (sample.rs:411-414)
+    // every non-history element >= th_raw is some chunk's candidate
+    const float th_raw = block_max(tid < nc ? mine.theta : -__builtin_inff(), sm.rf);
+    float th_m = -__builtin_inff();
+    if (C.mmode) {  // p >= min_p * max p needs s >= M + ln(min_p)
+        const float lm = logf(C.min_p);
+        th_m = M + lm - (1e-4f + 1e-5f * (fabsf(M) + fabsf(lm)));
+    }
+    float th = fmaxf(th_raw, th_m);
+    for (int pass = 0; pass < 2; pass++) {
+        // ---- the list: complete above th
+        // chunks whose own bound is above th (only in the repair pass) are re-read
+        const bool from_cands = tid < nc && mine.theta <= th && mine.m >= th;
+        uint32_t myn = from_cands ? mine.ncand : 0u;
+        uint32_t tot;
+        uint32_t off = block_excl_scan<uint32_t>(myn, sm.ru, tot);
+        if (tid < nc) sm.cpre[tid] = off;
+        if (tid == 0) {
+            sm.cpre[nc] = tot;
+            sm.misc[MISC_N] = 0;
+        }
+        __syncthreads();
+        const Cand* cands = a.cands + (int64_t)C.row * nc * CAND_CAP;
+        constexpr int GU = 4;  // loads in flight per thread
+        for (uint32_t f0 = tid; f0 < tot; f0 += GU * BLOCK) {
+            Cand cd[GU];
+#pragma unroll
+            for (int g = 0; g < GU; g++) {
+                const uint32_t f = f0 + g * BLOCK;
+                cd[g].idx = 0;
+                cd[g].s = -__builtin_inff();
+                if (f < tot) {
+                    int lo = 0, hi = nc;  // largest c with cpre[c] <= f
+                    while (hi - lo > 1) {
+                        int mid = (lo + hi) >> 1;
+                        if (sm.cpre[mid] <= f) lo = mid;
+                        else hi = mid;
+                    }
+                    cd[g] = cands[(int64_t)lo * CAND_CAP + (f - sm.cpre[lo])];
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < GU; g++) {
+                if (cd[g].s >= th && cd[g].s > -__builtin_inff() && !(C.pen_on && hist_find(sm, cd[g].idx) >= 0)) {
+                    uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+                    if (slot < NMAX)
+                        sm.u.cb.keys[slot] = sorted ? key64(cd[g].s, cd[g].idx)
+                                                    : (((uint64_t)(~cd[g].idx) << 32) | ord32(cd[g].s));
+                }
+            }
+        }
+        // history ids at their penalized values
+        for (int k = tid; k < HSLOTS; k += BLOCK) {
+            const uint32_t id = sm.hkey[k];
+            const float v = sm.hpen[k];
+            if (id != HEMPTY && v >= th && v > -__builtin_inff()) {
+                uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+                if (slot < NMAX) sm.u.cb.keys[slot] = sorted ? key64(v, id) : (((uint64_t)(~id) << 32) | ord32(v));
+            }
+        }
+        __syncthreads();
+        // re-read the chunks whose candidates stop above th (repair pass)
+        if (pass) {
+            for (int c = 0; c < nc; c++) {
+                const float tc = sm.cm[c] >= th ? a.parts[(int64_t)C.row * nc + c].theta : -__builtin_inff();
+                if (tc > th) rescan_collect<BF16, VEC>(a, sm, C, (uint32_t)c, th, sorted);
+            }
+            __syncthreads();
+        }
+        const int N = (int)sm.misc[MISC_N];
+        BFI_TRACE(a, tb, 2);
+        if (a.trace && tid == 0) a.trace[tb + 6] = ((uint64_t)tot << 32) | (uint32_t)N;
+        if (N > NMAX) return CB_RADIX;
+        const bool exhaustive = !(th > -__builtin_inff());
+        const bool minp_complete = th <= th_m;
+        if (N <= WAVE) {
+            if (combine_wave(a, sm, C, N, sorted, M, S, rawmax, exhaustive, minp_complete)) return CB_DONE;
+        } else {
+            const int r = combine_list(a, sm, C, N, sorted, M, S, rawmax, exhaustive, minp_complete, tb);
+            if (r >= 0) return r;
+        }
+        // the cut lies below th: list down to the min-p bound, or everything
+        th = C.mmode ? th_m : -__builtin_inff();
+    }
+    return CB_RADIX;
+}
+
+// ---- combine: draws in index order (no top-k/top-p) ------------------------------------
+//
+// Rows without top-k/top-p keep every element (or, with min-p, the retained ones) in index
+// order (sample.rs:411-414). The draw finds its chunk from per-chunk kept masses, then
+// re-reads that one chunk.
+
+// Kept weights of one tile of [t0, t1): p = expf(s - M) / S when p >= thresh, else 0
+// (and 0 outside the tile and for `excl`).
+template <bool BF16, int VEC>
+__device__ __forceinline__ void tile_weights(const KArgs& a, const Smem& sm, const RowCtx& C, const PenSrc& P,
+                                             uint32_t t0, uint32_t t1, float M, float S, float thresh, uint32_t excl,
+                                             float (&x)[VEC][Elem<BF16>::EPV]) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    load_tile<BF16, VEC>(a, C.row, t0, t1, x);
+    transform_tile<BF16, VEC>(sm, C, P, t0, t1, x);
+#pragma unroll
+    for (int q = 0; q < VEC; q++)
+#pragma unroll
+        for (int e = 0; e < EPV; e++) {
+            const uint32_t id = t0 + (uint32_t)(q * BLOCK + threadIdx.x) * EPV + e;
+            const float p = expf(x[q][e] - M) / S;
+            x[q][e] = (id < t1 && id != excl && p >= thresh) ? p : 0.0f;
+        }
+}
+
+// Re-reads chunk [c0, c1) and returns the first index (in index order) with a positive
+// weight where the cumulative weight reaches frac * (chunk total).
+template <bool BF16, int VEC>
+__device__ __forceinline__ uint32_t scan_chunk_index_order(const KArgs& a, Smem& sm, const RowCtx& C,
+                                                           const PenSrc& P, uint32_t c0, uint32_t c1, float M, float S,
+                                                           float thresh, uint32_t excl, double frac) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    constexpr uint32_t TILE = (uint32_t)BLOCK * VEC * EPV;
+    const int tid = threadIdx.x;
+    float x[VEC][EPV];
+    double tsum = 0.0;
+    for (uint32_t t0 = c0; t0 < c1; t0 += TILE) {
+        tile_weights<BF16, VEC>(a, sm, C, P, t0, min(t0 + TILE, c1), M, S, thresh, excl, x);
+#pragma unroll
+        for (int q = 0; q < VEC; q++)
+#pragma unroll
+            for (int e = 0; e < EPV; e++) tsum += x[q][e];
+    }
+    const double target = frac * block_sum_d(tsum, sm.rd);
+    double carry = 0.0;
+    uint32_t found = 0xFFFFFFFFu, lastpos = 0;
+    for (uint32_t t0 = c0; t0 < c1 && found == 0xFFFFFFFFu; t0 += TILE) {
+        const uint32_t t1 = min(t0 + TILE, c1);
+        tile_weights<BF16, VEC>(a, sm, C, P, t0, t1, M, S, thresh, excl, x);
+#pragma unroll
+        for (int q = 0; q < VEC; q++) {  // VEC slabs in index order
+            double ts = 0.0;
+#pragma unroll
+            for (int e = 0; e < EPV; e++) {
+                ts += x[q][e];
+                const uint32_t id = t0 + (uint32_t)(q * BLOCK + tid) * EPV + e;
+                if (x[q][e] > 0.0f) lastpos = max(lastpos, id + 1);
+            }
+            double tot;
+            const double pre = block_excl_scan<double>(ts, sm.rd, tot);
+            if (found == 0xFFFFFFFFu && carry + tot >= target) {
+                uint32_t best = 0xFFFFFFFFu;
+                double c = carry + pre;
+#pragma unroll
+                for (int e = 0; e < EPV; e++) {
+                    const uint32_t id = t0 + (uint32_t)(q * BLOCK + tid) * EPV + e;
+                    c += x[q][e];
+                    if (best == 0xFFFFFFFFu && x[q][e] > 0.0f && c >= target) best = id;
+                }
+                found = block_min_u(best, sm.ru);
+            }
+            carry += tot;
+        }
+    }
+    if (found == 0xFFFFFFFFu) {  // rounding at the chunk end: last positive element
+        const uint32_t l = (uint32_t)block_max_u64(lastpos, sm.r64);
+        found = l ? l - 1 : c0;
+    }
+    return found;
+}
+
+// Penalized value s of one element (the draft of a judged row).
+__device__ __forceinline__ float element_s(const KArgs& a, Smem& sm, const RowCtx& C, uint32_t id, bool bf16,
+                                           bool hashed) {
+    const int tid = threadIdx.x;
+    if (id >= (uint32_t)a.V) return -__builtin_inff();  // a draft outside the vocabulary
+    float x;
+    if (bf16)
+        x = __uint_as_float((uint32_t)((const uint16_t*)a.logits)[(int64_t)C.row * a.row_stride + id] << 16);
+    else
+        x = ((const float*)a.logits)[(int64_t)C.row * a.row_stride + id];
+    const bool allowed = !C.mrow || ((C.mrow[id >> 5] >> (id & 31)) & 1u);
+    uint32_t c = 0;
+    if (C.pen_on) {
+        if (hashed) {
+            const int k = hist_find(sm, id);
+            c = k >= 0 ? sm.hcnt[k] : 0u;
+        } else {
+            const int64_t H = C.h.size();
+            for (int64_t j = tid; j < H; j += BLOCK) c += C.h.at(j) == id;
+            c = block_sum_u(c, sm.ru);
+        }
+    }
+    return c ? pen_value(C, x, allowed, c) : raw_value(C, x, allowed);
+}
+
+// `mc` = this thread's chunk (tid < n_chunks) kept mass, normalized by S; `n_kept` = the
+// kept count (sample.rs:411-414; V when nothing is filtered).
+template <bool BF16, int VEC>
+__device__ __forceinline__ void combine_index_order(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P,
+                                                    bool hashed, float M, float S, float thresh, double mc,
+                                                    uint32_t n_kept) {
+    const int tid = threadIdx.x;
+    const int nc = a.n_chunks;
+    uint32_t pd_chunk = 0xFFFFFFFFu;
+    double p_d = 0.0;
+    if (C.judged && C.draft < (uint32_t)a.V) {
+        const float sd = element_s(a, sm, C, C.draft, BF16, hashed);
+        const float pf = expf(sd - M) / S;
+        if (pf >= thresh) {  // the draft is kept
+            p_d = (double)pf;
+            pd_chunk = C.draft / (uint32_t)a.chunk;
+            if ((uint32_t)tid == pd_chunk) mc = mc > p_d ? mc - p_d : 0.0;
+        }
+    }
+    double total;
+    const double pre = block_excl_scan<double>(tid < nc ? mc : 0.0, sm.rd, total);
+    const double sum = total + p_d;  // sum of kept weights
+    if (a.t_kind && tid == 0) {
+        a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
+        a.t_kept[C.row] = (int32_t)n_kept;
+        a.t_listed[C.row] = 0;
+    }
+    float u = C.u;
+    bool resid = false;
+    if (C.judged) {  // spec.rs:83-95
+        if (sum > 0.0 && (double)C.u < p_d / sum) {
+            emit(a, sm, C, C.draft, 1u);
+            return;
+        }
+        if (!(total > 0.0)) {  // residual empty or all <= 0
+            emit(a, sm, C, C.draft, 1u);
+            return;
+        }
+        u = C.u2;
+        resid = true;
+    }
+    const double r = (double)u * total;
+    uint32_t tok;
+    if (r <= 0.0 && thresh == 0.0f) {
+        // r = 0 picks the first element of the list, whatever its weight (sample.rs:314-319)
+        tok = (resid && C.draft == 0) ? 1u : 0u;
+    } else {
+        uint32_t c = 0xFFFFFFFFu;
+        if (tid < nc && mc > 0.0 && pre + mc >= r) c = (uint32_t)tid;
+        c = block_min_u(c, sm.ru);
+        if (c == 0xFFFFFFFFu) {  // rounding: last chunk with mass
+            uint32_t l = (tid < nc && mc > 0.0) ? (uint32_t)tid + 1 : 0u;
+            l = (uint32_t)block_max_u64(l, sm.r64);
+            c = l ? l - 1 : 0;
+        }
+        // mass before chunk c and the chunk's own mass
+        if ((uint32_t)tid == c) {
+            sm.rd[0] = pre;
+            sm.rd[1] = mc;
+        }
+        __syncthreads();
+        const double before = sm.rd[0], mass = sm.rd[1];
+        __syncthreads();
+        double frac = mass > 0.0 ? (r - before) / mass : 0.0;
+        frac = frac < 0.0 ? 0.0 : (frac > 1.0 ? 1.0 : frac);
+        tok = scan_chunk_index_order<BF16, VEC>(a, sm, C, P, chunk_lo(a, c), chunk_hi(a, c), M, S, thresh,
+                                                resid ? C.draft : 0xFFFFFFFFu, frac);
+    }
+    if (a.t_kind && tid == 0 && a.out_tok) a.out_tok[C.row] = tok;
+    emit(a, sm, C, tok, resid ? 0u : 1u);
+}
+
+// Index-order rows. `known` = this thread's chunk mass `mc` (normalized by S) is given
+// (unfiltered rows, from the streaming pass); otherwise one pass per chunk computes each
+// chunk's kept mass and count (min-p rows the candidate lists do not cover, rows with an
+// oversized history).
+template <bool BF16, int VEC>
+__device__ __forceinline__ void combine_index_order_passes(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P,
+                                                           bool hashed, float M, float S, ArgMax rawmax, bool known,
+                                                           double mc) {
+    const int tid = threadIdx.x;
+    const int nc = a.n_chunks;
+    const float thresh = C.mmode ? C.min_p * (1.0f / S) : 0.0f;  // sample.rs:411-414
+    uint32_t cnt = (uint32_t)a.V;
+    if (!known) {
+        mc = 0.0;
+        cnt = 0;
+        for (int c = 0; c < nc; c++) {
+            double w = 0.0;
+            span_pass<BF16, VEC, false>(a, sm, C, P, chunk_lo(a, c), chunk_hi(a, c), [&](uint32_t, float s) {
+                const float p = expf(s - M) / S;
+                if (p >= thresh) {
+                    w += (double)p;
+                    cnt++;
+                }
+            });
+            w = block_sum_d(w, sm.rd);
+            if (tid == c) mc = w;
+        }
+        cnt = block_sum_u(cnt, sm.ru);
+        if (C.mmode && cnt == 0) {  // sample.rs:415-422
+            finish_token(a, sm, C, rawmax.v > -__builtin_inff() ? rawmax.i : 0u);
+            return;
+        }
+    }
+    combine_index_order<BF16, VEC>(a, sm, C, P, hashed, M, S, thresh, mc, cnt);
+}
+
+// ---- combine: radix select over the row ------------------------------------------------
+
+struct Sel {
+    uint64_t key;       // selected element
+    uint64_t pos;       // its 0-based position in the sorted order
+    uint64_t cum_mass;  // fixed-point mass through it (inclusive)
+};
+
+// One pass over the whole row: f(id, s) for every element (s = penalized value).
+template <bool BF16, int VEC, typename F>
+__device__ __forceinline__ void row_pass(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, F f) {
+    span_pass<BF16, VEC, false>(a, sm, C, P, 0u, (uint32_t)a.V, f);
+}
+
+// Finds the element at a sorted position (kind 0: 0-based position `target`) or the first
+// element whose inclusive fixed-point cumulative mass reaches `target` (kind 1), over the
+// order of key64 descending, skipping the element with key `excl`.
+template <bool BF16, int VEC>
+__device__ __forceinline__ Sel radix_select(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, float M,
+                            double scale, int kind, uint64_t target, uint64_t excl, uint64_t excl_mass) {
+    const int tid = threadIdx.x;
+    uint64_t prefix = 0;
+    int pbits = 0;
+    uint64_t before_cnt = 0, before_mass = 0;
+    uint64_t* saved = a.row_hist + (int64_t)C.row * NBUCKET * 2;
+    for (int level = 0;; level++) {
+        const int w = (64 - pbits) >= 10 ? 10 : 64 - pbits;
+        const int shift = 64 - pbits - w;
+        const uint32_t nb = 1u << w;
+        if (level == 0) {  // the level-1 histogram saved by radix_l1 (minus `excl`)
+            for (uint32_t b = tid; b < NBUCKET; b += BLOCK) {
+                sm.u.hs.mass[b] = saved[2 * b];
+                sm.u.hs.cnt[b] = (uint32_t)saved[2 * b + 1];
+            }
+            __syncthreads();
+            if (excl != ~0ull && tid == 0) {
+                uint32_t b = (uint32_t)(excl >> 54);
+                sm.u.hs.cnt[b] -= 1;
+                sm.u.hs.mass[b] -= excl_mass;
+            }
+            __syncthreads();
+        } else {
+            for (uint32_t b = tid; b < NBUCKET; b += BLOCK) {
+                sm.u.hs.mass[b] = 0;
+                sm.u.hs.cnt[b] = 0;
+            }
+            __syncthreads();
+            row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) __attribute__((always_inline)) {
+                uint64_t k = key64(s, id);
+                if (k == excl) return;
+                if (pbits && (k >> (64 - pbits)) != prefix) return;
+                uint32_t b = (uint32_t)(k >> shift) & (nb - 1);
+                lds_add(&sm.u.hs.cnt[b], 1u);
+                uint64_t m = efix_of(s, M, scale);
+                if (m) lds_add64(&sm.u.hs.mass[b], m);
+            });
+            __syncthreads();
+        }
+        // scan buckets from the top (o = 0 is bucket nb-1); 4 buckets per thread
+        constexpr int BPT = NBUCKET / BLOCK;
+        uint64_t lc[BPT], lm[BPT];
+        uint64_t rc = 0, rm = 0;
+#pragma unroll
+        for (int i = 0; i < BPT; i++) {
+            uint32_t o = (uint32_t)tid * BPT + i;
+            uint32_t b = nb - 1 - o;
+            uint64_t c = o < nb ? sm.u.hs.cnt[b] : 0, m = o < nb ? sm.u.hs.mass[b] : 0;
+            rc += c;
+            rm += m;
+            lc[i] = rc;
+            lm[i] = rm;
+        }
+        uint64_t tc, tm;
+        uint64_t pc = block_excl_scan<uint64_t>(rc, sm.r64, tc);
+        uint64_t pm = block_excl_scan<uint64_t>(rm, sm.r64b, tm);
+        uint32_t hit = 0xFFFFFFFFu;
+#pragma unroll
+        for (int i = 0; i < BPT; i++) {
+            uint32_t o = (uint32_t)tid * BPT + i;
+            const uint32_t bc = o < nb ? sm.u.hs.cnt[nb - 1 - o] : 0u;
+            bool ok = kind == 0 ? (before_cnt + pc + lc[i] > target)
+                                : (bc > 0 && before_mass + pm + lm[i] >= target);
+            if (hit == 0xFFFFFFFFu && o < nb && ok) hit = o;
+        }
+        hit = block_min_u(hit, sm.ru);
+        if (hit == 0xFFFFFFFFu) {  // target beyond the total: the last non-empty bucket
+            uint32_t l = 0;
+            for (uint32_t o = tid; o < nb; o += BLOCK)
+                if (sm.u.hs.cnt[nb - 1 - o] > 0) l = max(l, o + 1);
+            l = (uint32_t)block_max_u64(l, sm.r64);
+            hit = l ? l - 1 : nb - 1;
+        }
+        // counts/mass above the chosen bucket
+        if ((uint32_t)tid == hit / BPT) {
+            const int i = (int)(hit % BPT);
+            uint64_t cab = pc, mab = pm;
+#pragma unroll
+            for (int ii = 0; ii < BPT; ii++) {
+                if (ii + 1 == i) {
+                    cab = pc + lc[ii];
+                    mab = pm + lm[ii];
+                }
+            }
+            sm.r64[0] = cab;
+            sm.r64b[0] = mab;
+            sm.r64[1] = sm.u.hs.cnt[nb - 1 - hit];
+        }
+        __syncthreads();
+        before_cnt += sm.r64[0];
+        before_mass += sm.r64b[0];
+        const uint64_t nbk = sm.r64[1];
+        __syncthreads();
+        prefix = (prefix << w) | (uint64_t)(nb - 1 - hit);
+        pbits += w;
+        if (nbk <= (uint64_t)NMAX || pbits >= 64) {
+            // gather the bucket, sort it, walk it
+            if (tid == 0) sm.misc[MISC_N] = 0;
+            __syncthreads();
+            row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) __attribute__((always_inline)) {
+                uint64_t k = key64(s, id);
+                if (k == excl) return;
+                if ((k >> (64 - pbits)) != prefix) return;
+                uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+                if (slot < NMAX) sm.u.cb.keys[slot] = k;
+            });
+            __syncthreads();
+            int N = (int)min(sm.misc[MISC_N], (uint32_t)NMAX);
+            int n2 = 64;
+            while (n2 < N) n2 <<= 1;
+            for (int j = N + tid; j < n2; j += BLOCK) sm.u.cb.keys[j] = 0ull;
+            __syncthreads();
+            bitonic_sort_desc(sm.u.cb.keys, n2);
+            // masses of the sorted bucket
+            uint64_t loc[PT];
+            uint64_t run = 0;
+#pragma unroll
+            for (int i = 0; i < PT; i++) {
+                int j = tid * PT + i;
+                run += j < N ? efix_of(key_s(sm.u.cb.keys[j]), M, scale) : 0ull;
+                loc[i] = run;
+            }
+            uint64_t tot;
+            uint64_t pre = block_excl_scan<uint64_t>(run, sm.r64, tot);
+            uint32_t best = 0xFFFFFFFFu;
+#pragma unroll
+            for (int i = 0; i < PT; i++) {
+                int j = tid * PT + i;
+                if (best != 0xFFFFFFFFu || j >= N) continue;
+                bool ok = kind == 0 ? (before_cnt + (uint64_t)j >= target)
+                                    : (before_mass + pre + loc[i] >= target);
+                if (ok) best = (uint32_t)j;
+            }
+            best = block_min_u(best, sm.ru);
+            if (best == 0xFFFFFFFFu) best = N > 0 ? (uint32_t)N - 1 : 0u;
+            Sel r;
+            if ((uint32_t)tid == best / PT) {
+                const int i = (int)(best % PT);
+                uint64_t li = 0;
+#pragma unroll
+                for (int ii = 0; ii < PT; ii++)
+                    if (ii == i) li = loc[ii];
+                sm.r64[0] = sm.u.cb.keys[best];
+                sm.r64[1] = before_mass + pre + li;
+            }
+            __syncthreads();
+            r.key = sm.r64[0];
+            r.cum_mass = sm.r64[1];
+            r.pos = before_cnt + best;
+            __syncthreads();
+            return r;
+        }
+    }
+}
+
+// Level-1 histogram (top 10 key bits) of the whole row, saved to global scratch for every
+// later query of this row; returns the total fixed-point mass.
+template <bool BF16, int VEC>
+__device__ __forceinline__ uint64_t radix_l1(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, float M, double scale) {
+    const int tid = threadIdx.x;
+    for (uint32_t b = tid; b < NBUCKET; b += BLOCK) {
+        sm.u.hs.mass[b] = 0;
+        sm.u.hs.cnt[b] = 0;
+    }
+    __syncthreads();
+    row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) __attribute__((always_inline)) {
+        uint32_t b = (uint32_t)(key64(s, id) >> 54);
+        lds_add(&sm.u.hs.cnt[b], 1u);
+        uint64_t m = efix_of(s, M, scale);
+        if (m) lds_add64(&sm.u.hs.mass[b], m);
+    });
+    __syncthreads();
+    uint64_t* saved = a.row_hist + (int64_t)C.row * NBUCKET * 2;
+    uint64_t m = 0;
+    for (uint32_t b = tid; b < NBUCKET; b += BLOCK) {
+        saved[2 * b] = sm.u.hs.mass[b];
+        saved[2 * b + 1] = sm.u.hs.cnt[b];
+        m += sm.u.hs.mass[b];
+    }
+    uint64_t tot;
+    block_excl_scan<uint64_t>(m, sm.r64, tot);
+    __threadfence_block();
+    __syncthreads();
+    return tot;
+}
+
+// Rows the candidate lists do not cover, in sorted order: top-k / top-p / min-p cuts and
+// the draw (sample.rs:392-426, 312-323) by radix queries over the row. The queries run
+// from one call site (a small state machine), which keeps the inlined code compact.
+template <bool BF16, int VEC>
+__device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, bool hashed,
+                                              float M, float S, ArgMax rawmax) {
+    const int tid = threadIdx.x;
+    const double scale = ldexp(1.0, a.fix_bits);
+    const uint64_t V = (uint64_t)a.V;
+
+    const uint64_t S_fix = radix_l1<BF16, VEC>(a, sm, C, P, M, scale);
+    const uint64_t Lk = C.kmode ? (uint64_t)C.k : V;
+    uint64_t Lp = ~0ull, Lm = ~0ull, L = 0, T = 0, kept_mass = 0, kd = ~0ull, md = 0;
+    Sel selp{0, 0, 0}, last{0, 0, 0};
+    if (C.pmode) {
+        const double tp = ceil((double)C.top_p * (double)S_fix);
+        T = tp <= 0.0 ? 0ull : (uint64_t)tp;
+    }
+    enum { Q_K, Q_P, Q_LAST, Q_DRAW, Q_RESID, ST_MINP, ST_LIST };
+    int st = C.pmode ? (C.kmode ? Q_K : Q_P) : ST_MINP;
+    for (;;) {
+        if (st == ST_MINP) {
+            if (C.mmode) {  // sample.rs:411-414: count p >= min_p * max_p
+                const float thresh = C.min_p * (1.0f / S);
+                uint32_t c = 0;
+                row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t, float s) { c += (expf(s - M) / S >= thresh) ? 1u : 0u; });
+                Lm = block_sum_u(c, sm.ru);
+                if (Lm == 0) {  // sample.rs:415-422
+                    finish_token(a, sm, C, rawmax.v > -__builtin_inff() ? rawmax.i : 0u);
+                    return;
+                }
+            }
+            L = Lk < Lp ? Lk : Lp;
+            L = L < Lm ? L : Lm;
+            if (C.pmode && L == Lp) {
+                last = selp;
+                st = ST_LIST;
+            } else {
+                st = Q_LAST;
+            }
+            continue;
+        }
+        if (st == ST_LIST) {
+            kept_mass = last.cum_mass;
+            if (a.t_kind && tid == 0) {
+                a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
+                a.t_kept[C.row] = (int32_t)L;
+                a.t_listed[C.row] = 0;
+            }
+            // introspection listing: gather keys >= last.key when they fit
+            if (a.t_kind && a.t_cap > 0 && L <= (uint64_t)NMAX) {
+                if (tid == 0) sm.misc[MISC_N] = 0;
+                __syncthreads();
+                row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) {
+                    const uint64_t k = key64(s, id);
+                    if (k >= last.key) {
+                        const uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+                        if (slot < NMAX) sm.u.cb.keys[slot] = k;
+                    }
+                });
+                __syncthreads();
+                const int N = (int)min(sm.misc[MISC_N], (uint32_t)NMAX);
+                int n2 = 64;
+                while (n2 < N) n2 <<= 1;
+                for (int j = N + tid; j < n2; j += BLOCK) sm.u.cb.keys[j] = 0ull;
+                __syncthreads();
+                bitonic_sort_desc(sm.u.cb.keys, n2);
+                uint32_t c = 0;
+                for (int j = tid * PT; j < tid * PT + PT; j++)
+                    if (j < N) c += (expf(key_s(sm.u.cb.keys[j]) - M) / S) > 0.0f;
+                uint32_t tc;
+                uint32_t o = block_excl_scan<uint32_t>(c, sm.ru, tc);
+                for (int j = tid * PT; j < tid * PT + PT; j++) {
+                    if (j < N) {
+                        const float pj = expf(key_s(sm.u.cb.keys[j]) - M) / S;
+                        if (pj > 0.0f) {
+                            if ((int64_t)o < a.t_cap) {
+                                a.t_ids[(int64_t)C.row * a.t_cap + o] = key_idx(sm.u.cb.keys[j]);
+                                a.t_probs[(int64_t)C.row * a.t_cap + o] = pj;
+                            }
+                            o++;
+                        }
+                    }
+                }
+                if (tid == 0) a.t_listed[C.row] = (int32_t)(tc < a.t_cap ? tc : a.t_cap);
+                __syncthreads();
+            }
+            if (!C.judged) {
+                st = Q_DRAW;
+                continue;
+            }
+            // judge (spec.rs:83-95)
+            const float sd = element_s(a, sm, C, C.draft, BF16, hashed);
+            const bool kept_d = C.draft < V && key64(sd, C.draft) >= last.key;
+            kd = kept_d ? key64(sd, C.draft) : ~0ull;
+            md = kept_d ? efix_of(sd, M, scale) : 0ull;
+            if (kept_mass > 0 && (double)C.u < (double)md / (double)kept_mass) {
+                emit(a, sm, C, C.draft, 1u);
+                return;
+            }
+            if (kept_mass - md == 0) {  // residual empty or all <= 0
+                emit(a, sm, C, C.draft, 1u);
+                return;
+            }
+            st = Q_RESID;
+            continue;
+        }
+        // one radix query
+        int kind = 1;
+        uint64_t target = 0, ex = ~0ull, exm = 0;
+        if (st == Q_K) {
+            kind = 0;
+            target = Lk - 1;
+        } else if (st == Q_P) {
+            target = T;
+        } else if (st == Q_LAST) {
+            kind = 0;
+            target = L - 1;
+        } else if (st == Q_DRAW) {
+            target = (uint64_t)ceil((double)C.u * (double)kept_mass);
+        } else {
+            target = (uint64_t)ceil((double)C.u2 * (double)(kept_mass - md));
+            ex = kd;
+            exm = md;
+        }
+        const Sel r = radix_select<BF16, VEC>(a, sm, C, P, M, scale, kind, target, ex, exm);
+        if (st == Q_K) {  // top-p runs over the top-k list: cut inside it, or keep all k
+            if (r.cum_mass < T) {
+                Lp = Lk;
+                selp = r;
+                st = ST_MINP;
+            } else {
+                st = Q_P;
+            }
+        } else if (st == Q_P) {
+            selp = r;
+            Lp = r.pos + 1;
+            st = ST_MINP;
+        } else if (st == Q_LAST) {
+            last = r;
+            st = ST_LIST;
+        } else {
+            const uint32_t tok = key_idx(r.key);
+            if (st == Q_DRAW && a.t_kind && tid == 0 && a.out_tok) a.out_tok[C.row] = tok;
+            emit(a, sm, C, tok, st == Q_DRAW ? 1u : 0u);
+            return;
+        }
+    }
+}
+
+// ---- select kernel: one workgroup per row ----------------------------------------------
+//
+// The streaming pass saw every element at its un-penalized value. The select kernel puts
+// the row's history ids (at most HMAX distinct) in an LDS hash, computes their penalized
+// values, and corrects the chunk statistics: a history id's term exp(s - m_c) is taken out
+// of its chunk's sum (recomputed exactly as the streaming pass did, accumulated in fixed
+// point so the result does not depend on the order), and its penalized term is added. A
+// chunk whose maximum is a history id ("dirty") is re-read for the maximum and sum of its
+// other elements, so that no subtraction loses precision. Rows with a larger history take
+// whole-row passes with the history tables in global memory.
+
+constexpr double FIX52 = 4503599627370496.0;  // 2^52: fixed-point scale of the corrections
+
+// Every logit is -inf: the reference's weights are NaN and its outcome is deterministic
+// (the min-p fallback argmax, or the last kept id of the draw).
+__device__ __forceinline__ void finish_all_masked(const KArgs& a, Smem& sm, const RowCtx& C, ArgMax rawmax) {
+    if (C.mmode) {
+        finish_token(a, sm, C, rawmax.v > -__builtin_inff() ? rawmax.i : 0u);
+        return;
+    }
+    const uint32_t L = C.kmode ? (uint32_t)C.k : (uint32_t)a.V;
+    if (a.t_kind && threadIdx.x == 0) {
+        a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
+        a.t_kept[C.row] = (int32_t)L;
+        a.t_listed[C.row] = 0;
+    }
+    if (C.judged) {
+        // residual = kept minus d; a draw over NaN weights returns its last id
+        const uint32_t lastid = (C.draft == L - 1) ? L - 2 : L - 1;
+        const bool empty = (L == 1 && C.draft == 0);
+        emit(a, sm, C, empty ? C.draft : lastid, empty ? 1u : 0u);
+        return;
+    }
+    if (a.t_kind && threadIdx.x == 0 && a.out_tok) a.out_tok[C.row] = L - 1;
+    emit(a, sm, C, L - 1, 1u);
+}
+
+// Rows whose history does not fit the hash: M (greedy: the argmax) and S by whole-row
+// passes with the history tables in global memory. Returns false when the row is done.
+template <bool BF16, int VEC>
+__device__ __forceinline__ bool stats_full(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, ArgMax rawmax,
+                                           float& M, float& S) {
+    ArgMax am{-__builtin_inff(), 0xFFFFFFFFu};
+    row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) { am = argmax_merge(am, ArgMax{s, id}); });
+    am = block_argmax(am, sm.rf, sm.ru);
+    if (C.greedy) {  // sample.rs:369-371, 429-439
+        finish_token(a, sm, C, am.v > -__builtin_inff() ? am.i : 0u);
+        return false;
+    }
+    M = am.v;
+    if (!(M > -__builtin_inff())) {
+        finish_all_masked(a, sm, C, rawmax);
+        return false;
+    }
+    double ls = 0.0;
+    row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t, float s) { ls += (double)expf(s - M); });
+    S = (float)block_sum_d(ls, sm.rd);
+    return true;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
+    constexpr int VEC = BF16 ? 2 : 4;  // row passes walk 4096-element tiles
+    __shared__ Smem sm;
+    const int tid = threadIdx.x;
+    // rows grouped per XCD (dispatch is round-robin over the 8 XCDs)
+    const uint32_t G = gridDim.x, bid = blockIdx.x;
+    const uint32_t q8 = G / 8, r8 = G % 8, xcd = bid % 8, slot = bid / 8;
+    const int row = (int)(xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot);
+    const int64_t tb = ((int64_t)a.n_rows * a.n_chunks + row) * 8;
+    BFI_TRACE(a, tb, 0);
+    if (row >= a.n_rows) return;
+    const RowCtx C = make_ctx(a, row);
+    if (!C.active) return;
+    const bool track_raw = !C.greedy && C.min_p > 1.0f;
+
+    const int nc = a.n_chunks;
+    ChunkPart mine;
+    if (tid < nc) {
+        mine = a.parts[(int64_t)row * nc + tid];
+    } else {
+        mine.m = -__builtin_inff();
+        mine.sum = 0.0;
+        mine.arg = 0xFFFFFFFFu;
+        mine.ncand = 0;
+        mine.theta = -__builtin_inff();
+        mine.raw_m = -__builtin_inff();
+        mine.raw_arg = 0xFFFFFFFFu;
+    }
+    ArgMax rawmax{-__builtin_inff(), 0xFFFFFFFFu};  // masked, un-penalized (sample.rs:415-422)
+    if (track_raw) rawmax = block_argmax(ArgMax{mine.raw_m, mine.raw_arg}, sm.rf, sm.ru);
+
+    const bool hashed = hist_build(a, sm, C);
+    const PenSrc H{true, nullptr, nullptr, nullptr};
+    const int nw = a.bm_words;
+    const uint32_t* gbm = a.row_pen + (int64_t)row * (2 * nw + GDCAP);
+    const PenSrc GT{false, gbm, gbm + nw, gbm + 2 * nw};
+    float M, S;
+    double wc = 0.0;  // this thread's chunk: sum of exp(s - M) (hashed rows)
+    enum { R_INDEX, R_RADIX };
+    int route;
+    if (!hashed) {
+        build_row_pen(a, sm, C);
+        if (!stats_full<BF16, VEC>(a, sm, C, GT, rawmax, M, S)) return;
+        if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 4.0f;
+        route = (C.kmode || C.pmode) ? R_RADIX : R_INDEX;
+    } else {
+        if (tid < nc) {
+            sm.cm[tid] = mine.m;
+            sm.carg[tid] = mine.arg;
+            sm.csum[tid] = mine.sum;
+            sm.cflag[tid] = 0u;
+            sm.craw[tid] = 0ull;
+            sm.cpen[tid] = 0ull;
+        }
+        __syncthreads();
+        // history values: as the streaming pass saw them, and penalized (sample.rs:331-375)
+        float hmax = -__builtin_inff();
+        uint32_t dirty = 0;
+        if (C.pen_on) {
+            for (int k = tid; k < HSLOTS; k += BLOCK) {
+                const uint32_t id = sm.hkey[k];
+                if (id == HEMPTY) continue;
+                float x;
+                if (BF16)
+                    x = __uint_as_float((uint32_t)((const uint16_t*)a.logits)[(int64_t)row * a.row_stride + id] << 16);
+                else
+                    x = ((const float*)a.logits)[(int64_t)row * a.row_stride + id];
+                const bool allowed = !C.mrow || ((C.mrow[id >> 5] >> (id & 31)) & 1u);
+                const float vr = raw_value(C, x, allowed), vp = pen_value(C, x, allowed, sm.hcnt[k]);
+                sm.hraw[k] = vr;
+                sm.hpen[k] = vp;
+                hmax = fmaxf(hmax, vp);
+                if (vr > -__builtin_inff()) lds_max(&sm.cflag[id / (uint32_t)a.chunk], ord32(vr));
+            }
+            __syncthreads();
+            // dirty: a history id holds the chunk's maximum
+            if (tid < nc && sm.cflag[tid] != 0u && mine.m > -__builtin_inff() && unord32(sm.cflag[tid]) == mine.m)
+                dirty = 1u;
+            const uint32_t nd = block_sum_u(dirty, sm.ru);
+            if (tid < nc) sm.cflag[tid] = dirty;
+            __syncthreads();
+            if (nd) {
+                BFI_TRACE(a, tb, 5);
+                for (int c = 0; c < nc; c++) {
+                    if (!sm.cflag[c]) continue;
+                    ArgMax am{-__builtin_inff(), 0xFFFFFFFFu};
+                    span_pass<BF16, VEC, true>(a, sm, C, H, chunk_lo(a, c), chunk_hi(a, c),
+                                               [&](uint32_t id, float v) { am = argmax_merge(am, ArgMax{v, id}); });
+                    am = block_argmax(am, sm.rf, sm.ru);
+                    double ls = 0.0;
+                    if (!C.greedy && am.v > -__builtin_inff())
+                        span_pass<BF16, VEC, true>(a, sm, C, H, chunk_lo(a, c), chunk_hi(a, c),
+                                                   [&](uint32_t, float v) { ls += (double)__expf(v - am.v); });
+                    ls = block_sum_d(ls, sm.rd);
+                    if (tid == 0) {
+                        sm.cm[c] = am.v;
+                        sm.carg[c] = am.i;
+                        sm.csum[c] = ls;
+                    }
+                }
+                __syncthreads();
+                if (tid < nc && dirty) {
+                    mine.m = sm.cm[tid];
+                    mine.arg = sm.carg[tid];
+                    mine.sum = sm.csum[tid];
+                }
+            }
+        }
+        if (C.greedy) {  // sample.rs:369-371, 429-439
+            ArgMax am{tid < nc ? mine.m : -__builtin_inff(), tid < nc ? mine.arg : 0xFFFFFFFFu};
+            if (C.pen_on)
+                for (int k = tid; k < HSLOTS; k += BLOCK)
+                    if (sm.hkey[k] != HEMPTY) am = argmax_merge(am, ArgMax{sm.hpen[k], sm.hkey[k]});
+            am = block_argmax(am, sm.rf, sm.ru);
+            finish_token(a, sm, C, am.v > -__builtin_inff() ? am.i : 0u);
+            return;
+        }
+        M = block_max(fmaxf(tid < nc ? mine.m : -__builtin_inff(), hmax), sm.rf);
+        if (!(M > -__builtin_inff())) {
+            finish_all_masked(a, sm, C, rawmax);
+            return;
+        }
+        // corrections: out with the streaming terms of the history ids of clean chunks, in
+        // with their penalized terms
+        if (C.pen_on) {
+            for (int k = tid; k < HSLOTS; k += BLOCK) {
+                const uint32_t id = sm.hkey[k];
+                if (id == HEMPTY) continue;
+                const uint32_t c = id / (uint32_t)a.chunk;
+                if (!sm.cflag[c]) {
+                    const float mc = sm.cm[c];
+                    if (mc > -__builtin_inff()) {
+                        const double t = (double)__expf(sm.hraw[k] - mc);  // as the streaming pass
+                        lds_add64(&sm.craw[c], (uint64_t)(t * FIX52));
+                    }
+                }
+                const double tp = (double)expf(sm.hpen[k] - M);
+                lds_add64(&sm.cpen[c], (uint64_t)(tp * FIX52));
+            }
+            __syncthreads();
+        }
+        if (tid < nc) {
+            if (mine.m > -__builtin_inff()) {
+                const double rc = mine.sum - (C.pen_on && !dirty ? (double)sm.craw[tid] / FIX52 : 0.0);
+                wc = rc * (double)expf(mine.m - M);
+            }
+            if (C.pen_on) wc += (double)sm.cpen[tid] / FIX52;
+        }
+        S = (float)block_sum_d(wc, sm.rd);
+        BFI_TRACE(a, tb, 1);
+        uint32_t flags = 0;  // some chunk unbounded/overflowed
+        if (tid < nc && (mine.ncand == NCAND_UNBOUNDED || mine.ncand == NCAND_OVERFLOW)) flags = 1;
+        flags = block_sum_u(flags, sm.ru);
+        if (!C.kmode && !C.pmode && !C.mmode) {
+            if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 2.0f;
+            route = R_INDEX;
+        } else {
+            if (flags == 0) {
+                if (a.t_stats && tid == 0) {
+                    a.t_stats[row * 4 + 0] = M;
+                    a.t_stats[row * 4 + 1] = S;
+                    a.t_stats[row * 4 + 3] = 1.0f;
+                }
+                if (combine_bounded<BF16, VEC>(a, sm, C, mine, M, S, rawmax, tb) == CB_DONE) {
+                    BFI_TRACE(a, tb, 7);
+                    return;
+                }
+            }
+            if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 3.0f;
+            route = (C.kmode || C.pmode) ? R_RADIX : R_INDEX;
+        }
+    }
+    if (a.t_stats && tid == 0) {
+        a.t_stats[row * 4 + 0] = M;
+        a.t_stats[row * 4 + 1] = S;
+    }
+    if (route == R_RADIX) {
+        if (hashed) build_row_pen(a, sm, C);
+        combine_radix<BF16, VEC>(a, sm, C, GT, hashed, M, S, rawmax);
+    } else {
+        const bool known = hashed && !C.kmode && !C.pmode && !C.mmode;
+        combine_index_order_passes<BF16, VEC>(a, sm, C, hashed ? H : GT, hashed, M, S, rawmax, known,
+                                              known ? wc / (double)S : 0.0);
+    }
+}
+
+// ---- launch ----------------------------------------------------------------------------
+
+hipError_t launch_select(const KArgs& a, int bf16, hipStream_t stream) {
+    const dim3 grid((unsigned)a.n_rows), block(BLOCK);
+    if (bf16)
+        hipLaunchKernelGGL((k_select<true>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((k_select<false>), grid, block, 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace bfi

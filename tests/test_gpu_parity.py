@@ -292,3 +292,94 @@ def test_repeated_launches_are_deterministic(smp):
     torch.cuda.synchronize()
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
+
+
+# ---- history corrections, fallback paths, magnitudes ---------------------------------------
+
+MODES = [
+    dict(temperature=0.0),
+    dict(temperature=0.9, top_k=50),
+    dict(temperature=0.9, top_p=0.9),
+    dict(temperature=0.9, min_p=0.05),
+    dict(temperature=0.9),
+    dict(temperature=0.9, min_p=0.05, top_p=0.95),
+    dict(temperature=0.9, top_k=20, top_p=0.8, min_p=0.02),
+]
+PENALTIES = [
+    dict(repeat_penalty=1.5),
+    dict(repeat_penalty=0.7),
+    dict(presence_penalty=-0.8, frequency_penalty=0.2),
+    dict(repeat_penalty=1.3, presence_penalty=0.5, frequency_penalty=0.4),
+]
+
+
+def test_history_holds_chunk_maxima(smp):
+    """Histories made of each row's largest logits: most chunks' maxima are penalized, so the
+    select pass re-derives those chunks' statistics."""
+    rng = np.random.default_rng(11)
+    V = 50000
+    params, hist, rows = [], [], []
+    for m in MODES:
+        for p in PENALTIES:
+            x = (rng.standard_normal(V) * 2).astype(np.float32)
+            top = np.argsort(-x, kind="stable")[:300]
+            h = np.concatenate([top, top[:40], top[:10]]).astype(np.uint32)  # repeats for counts
+            rng.shuffle(h)
+            rows.append(x)
+            hist.append(h.tolist())
+            params.append({**m, **p})
+    u = rng.random(len(rows)).astype(np.float32)
+    cfg = _cfg_from(rows, params, hist, u=u.tolist())
+    cfg["name"] = "dirty-chunks"
+    check(cfg, 512, smp)
+
+
+def test_history_larger_than_the_hash(smp):
+    """More distinct history ids than the select pass's LDS hash holds: whole-row passes."""
+    rng = np.random.default_rng(12)
+    V = 30000
+    params, hist, rows = [], [], []
+    for m in MODES:
+        x = (rng.standard_normal(V) * 2).astype(np.float32)
+        ids = rng.choice(V, 3000, replace=False)
+        h = np.concatenate([ids, ids[:700], np.argsort(-x)[:20]]).astype(np.uint32)
+        rows.append(x)
+        hist.append(h.tolist())
+        params.append({**m, "repeat_penalty": 1.2, "presence_penalty": 0.3, "frequency_penalty": 0.1})
+    u = rng.random(len(rows)).astype(np.float32)
+    cfg = _cfg_from(rows, params, hist, u=u.tolist())
+    cfg["name"] = "large-history"
+    check(cfg, 512, smp)
+
+
+def test_min_p_only_rows_beyond_the_candidate_lists(smp):
+    """Flat rows under min-p alone keep most of the vocabulary, in index order."""
+    rng = np.random.default_rng(13)
+    V = 75968
+    rows = [(rng.standard_normal(V) * 0.05).astype(np.float32) for _ in range(4)]
+    params = [dict(temperature=1.0, min_p=0.05), dict(temperature=0.5, min_p=0.9),
+              dict(temperature=1.0, min_p=0.05, repeat_penalty=1.3), dict(temperature=2.0, min_p=0.5)]
+    hist = [[], [], rng.choice(V, 500, replace=False).tolist(), []]
+    cfg = _cfg_from(rows, params, hist, u=[0.0, 0.5, 0.77, 0.999])
+    cfg["name"] = "min-p-flat"
+    check(cfg, 256, smp)
+
+
+def test_extreme_magnitudes(smp):
+    """Logits outside [2^-100, 2^100) take IEEE division; the values must match it exactly."""
+    rng = np.random.default_rng(14)
+    V = 20000
+    rows = []
+    for k in range(4):
+        x = rng.standard_normal(V).astype(np.float32)
+        x[rng.choice(V, 50, replace=False)] = np.float32(1e-35)
+        x[rng.choice(V, 50, replace=False)] = np.float32(-3e-39)
+        if k % 2:
+            x[rng.choice(V, 3, replace=False)] = np.float32(2.0 ** 110)
+            x[rng.choice(V, 3, replace=False)] = np.float32(-(2.0 ** 120))
+        rows.append(x)
+    params = [dict(temperature=0.7, top_k=40), dict(temperature=0.7, top_p=0.9), dict(temperature=1.3),
+              dict(temperature=0.7, min_p=0.1)]
+    cfg = _cfg_from(rows, params, u=[0.3, 0.6, 0.9, 0.1])
+    cfg["name"] = "magnitudes"
+    check(cfg, 256, smp)
