@@ -15,8 +15,8 @@
 #include <vector>
 
 namespace bfi {
-hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream);
-hipError_t launch_select(const KArgs& a, int bf16, hipStream_t stream);
+hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+hipError_t launch_select(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 }
 
 struct bfi_smp_ctx {
@@ -34,7 +34,7 @@ struct bfi_smp_ctx {
     uint64_t* trace = nullptr;
     size_t trace_words = 0, trace_used = 0;
     bool tracing = false;
-    // profiling: event triples around (k_stream, k_select) of each launch
+    // profiling: per launch, start/stop events recorded in the dispatches of k_stream and k_select
     bool profiling = false;
     std::vector<hipEvent_t> ev_pool;
     size_t ev_used = 0;
@@ -97,7 +97,7 @@ bool choose_shape(int64_t n_rows, int64_t V, int bf16, Shape& s) {
     for (int i = 0; i < 3; i++) {
         int chunk = bfi::BLOCK * vecs[i] * epv;
         int64_t nc = (V + chunk - 1) / chunk;
-        if (nc > bfi::BLOCK) continue;
+        if (nc > bfi::NCMAX) continue;
         s = Shape{vecs[i], chunk, (int)nc};
         found = true;
         if (n_rows * nc >= 1024) break;
@@ -283,27 +283,26 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
         a.trace = ctx->trace;
     }
 
-    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     if (ctx->profiling) {
-        if (ctx->ev_used + 3 > ctx->ev_pool.size()) {
-            if (ctx->ev_pool.size() >= 3 * 65536) return fail(ctx, BFI_SMP_EINVAL, "profiling record full: read it");
-            for (int i = 0; i < 3 * 256; i++) {
+        if (ctx->ev_used + 4 > ctx->ev_pool.size()) {
+            if (ctx->ev_pool.size() >= 4 * 65536) return fail(ctx, BFI_SMP_EINVAL, "profiling record full: read it");
+            for (int i = 0; i < 4 * 256; i++) {
                 hipEvent_t x;
                 hipError_t ee = hipEventCreate(&x);
                 if (ee != hipSuccess) return hip_fail(ctx, ee, "hipEventCreate");
                 ctx->ev_pool.push_back(x);
             }
         }
-        for (int i = 0; i < 3; i++) ev[i] = ctx->ev_pool[ctx->ev_used + i];
-        ctx->ev_used += 3;
+        for (int i = 0; i < 4; i++) ev[i] = ctx->ev_pool[ctx->ev_used + i];
+        ctx->ev_used += 4;
     }
     const int bf16 = c.dtype == BFI_SMP_BF16;
     hipError_t e = hipSuccess;
-    if (ev[0] && (e = hipEventRecord(ev[0], stream)) != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
-    if ((e = bfi::launch_stream(a, bf16, s.vec, stream)) != hipSuccess) return hip_fail(ctx, e, "k_stream launch");
-    if (ev[1] && (e = hipEventRecord(ev[1], stream)) != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
-    if ((e = bfi::launch_select(a, bf16, stream)) != hipSuccess) return hip_fail(ctx, e, "k_select launch");
-    if (ev[2] && (e = hipEventRecord(ev[2], stream)) != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
+    if ((e = bfi::launch_stream(a, bf16, s.vec, stream, ev[0], ev[1])) != hipSuccess)
+        return hip_fail(ctx, e, "k_stream launch");
+    if ((e = bfi::launch_select(a, bf16, stream, ev[2], ev[3])) != hipSuccess)
+        return hip_fail(ctx, e, "k_select launch");
     return BFI_SMP_OK;
 }
 
@@ -369,14 +368,14 @@ int bfi_smp_profile(bfi_smp_ctx* ctx, double* stream_ms, double* select_ms, int6
     if (!ctx || !stream_ms || !select_ms || !launches) return fail(ctx, BFI_SMP_EINVAL, "NULL argument");
     DeviceGuard g(ctx->device);
     double a = 0.0, b = 0.0;
-    const size_t n = ctx->ev_used / 3;
+    const size_t n = ctx->ev_used / 4;
     for (size_t i = 0; i < n; i++) {
-        hipEvent_t* e = &ctx->ev_pool[3 * i];
-        hipError_t r = hipEventSynchronize(e[2]);
+        hipEvent_t* e = &ctx->ev_pool[4 * i];
+        hipError_t r = hipEventSynchronize(e[3]);
         if (r != hipSuccess) return hip_fail(ctx, r, "hipEventSynchronize");
         float t1 = 0.0f, t2 = 0.0f;
         if ((r = hipEventElapsedTime(&t1, e[0], e[1])) != hipSuccess) return hip_fail(ctx, r, "hipEventElapsedTime");
-        if ((r = hipEventElapsedTime(&t2, e[1], e[2])) != hipSuccess) return hip_fail(ctx, r, "hipEventElapsedTime");
+        if ((r = hipEventElapsedTime(&t2, e[2], e[3])) != hipSuccess) return hip_fail(ctx, r, "hipEventElapsedTime");
         a += t1;
         b += t2;
     }

@@ -16,7 +16,9 @@ struct RowCtx {
     uint32_t draft;
     float u, u2;
     float T, rT, top_p, min_p;
-    bool fast_div;  // T in [2^-20, 2^20]: FMA-corrected reciprocal division is exact
+    float rTl;  // log2(e) / T (the streaming pass's exp scale)
+    bool fast_div;   // T in [2^-20, 2^20]: FMA-corrected reciprocal division is exact
+    bool stream_ok;  // T in [2^-125, 2^125]: the streaming pass's bounds and terms are usable
     int32_t k;
     bool greedy, kmode, pmode, mmode;
     Pen pen;
@@ -74,7 +76,9 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
     const int64_t H = C.h.size();
     C.T = P.temperature;
     C.rT = 1.0f / P.temperature;  // IEEE, once per row
+    C.rTl = C.rT * 1.44269504088896341f;
     C.fast_div = P.temperature >= 0x1p-20f && P.temperature <= 0x1p20f;
+    C.stream_ok = P.temperature >= 0x1p-125f && P.temperature <= 0x1p125f;
     C.top_p = P.top_p;
     C.min_p = P.min_p;
     C.k = P.top_k;
@@ -199,14 +203,31 @@ __device__ __forceinline__ float pen_value(const RowCtx& C, float x, bool allowe
 
 // ---- small helpers ---------------------------------------------------------------------
 
+// The streaming pass works on masked logits x. Its exp-sum term of x in a chunk whose
+// largest masked logit is xm is 2^((x - xm) * (log2(e) / T)): x - xm is exact near the
+// maximum (Sterbenz), so the large terms carry only the rounding of the scale and of
+// v_exp_f32; the select kernel recomputes the terms of history ids with the same
+// expression. Exact values x / T (div_T) are computed only where they are kept.
+__device__ __forceinline__ float stream_term(const RowCtx& C, float x, float xm) {
+    return __builtin_amdgcn_exp2f((x - xm) * C.rTl);
+}
+// A bound t on exact values x / T as a bound on masked logits: every x whose exact value
+// is >= t is >= x_bound(t) (the product t * T, lowered by 2^-20 relative).
+__device__ __forceinline__ float x_bound(const RowCtx& C, float t) {
+    const float b = t * C.T;
+    const float w = b - (fabsf(b) * 0x1p-20f + 0x1p-126f);
+    return w == w ? w : b;  // +-inf stays
+}
+
+// Finite masked logits of a tile that are >= xth.
 template <bool BF16, int VEC>
-__device__ __forceinline__ uint32_t tile_count_ge(const float (&x)[VEC][Elem<BF16>::EPV], float th) {
+__device__ __forceinline__ uint32_t tile_count_ge(const float (&x)[VEC][Elem<BF16>::EPV], float xth) {
     constexpr int EPV = Elem<BF16>::EPV;
     uint32_t c = 0;
 #pragma unroll
     for (int q = 0; q < VEC; q++)
 #pragma unroll
-        for (int e = 0; e < EPV; e++) c += (x[q][e] >= th && x[q][e] > -__builtin_inff()) ? 1u : 0u;
+        for (int e = 0; e < EPV; e++) c += (x[q][e] >= xth && x[q][e] > -__builtin_inff()) ? 1u : 0u;
     return c;
 }
 

@@ -12,10 +12,16 @@
 
 namespace bfi {
 
-constexpr int BLOCK = 256;  // threads per workgroup (4 wave64s)
+// Threads per workgroup: each kernel's translation unit may set BFI_BLOCK before including
+// this header (the streaming kernel uses 256 = 4 wave64s).
+#ifndef BFI_BLOCK
+#define BFI_BLOCK 256
+#endif
+constexpr int BLOCK = BFI_BLOCK;
 constexpr int WAVE = 64;
 constexpr int NWAVE = BLOCK / WAVE;
 constexpr int CHUNK_MAX = 8192;        // logits elements per workgroup (stream phase)
+constexpr int NCMAX = 256;             // chunks per row
 constexpr int CAND_CAP = 2048;         // candidates one chunk may hand to the combine
 constexpr int NMAX = 2048;             // combine sort capacity (power of two)
 constexpr int NBUCKET = 1024;          // radix buckets (10-bit digits) of the fallback select
@@ -29,23 +35,24 @@ constexpr uint32_t NCAND_UNBOUNDED = 0xFFFFFFFFu;  // row has no top-k / min-p b
 constexpr uint32_t NCAND_OVERFLOW = 0xFFFFFFFEu;   // chunk had more than CAND_CAP candidates
 constexpr float F32_EPS = 1.1920928955078125e-07f;  // f32::EPSILON
 
-// Per (row, chunk) result of the streaming pass, over un-penalized values s = masked/T
-// (greedy: masked logits).
+// Per (row, chunk) result of the streaming pass over un-penalized values s = masked x / T
+// (greedy: the masked logits).
 struct ChunkPart {
-    float m;          // max of s
+    float m;          // max of s (exact)
     uint32_t arg;     // greedy: first index attaining m
-    double sum;       // sum of the f32 terms __expf(s - m), accumulated in f64
+    double sum;       // sum of stream_term over the chunk (f64 over per-vector f32 sums)
     uint32_t ncand;   // candidates written, or NCAND_UNBOUNDED / NCAND_OVERFLOW
     float theta;      // every element of the chunk with finite s >= theta was written
-    float raw_m;      // max of masked, un-penalized logits (only when min_p > 1)
-    uint32_t raw_arg; // its first index
+    float raw_m;      // max of the masked logits (the terms' reference point)
+    uint32_t raw_arg; // its first index (greedy rows and rows with min_p > 1)
     uint32_t pad;
     uint32_t pad2;
 };
 
+// A candidate of the kept set: its index and masked logit (the select kernel divides by T).
 struct Cand {
     uint32_t idx;
-    float s;
+    float x;
 };
 
 // Everything a launch needs; passed by value.

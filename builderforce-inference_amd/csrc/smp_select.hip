@@ -13,6 +13,11 @@
 //     masses), re-reading the row.
 // Spec verify applies judge() (spec.rs:79-97) to each row's target; the last row of a
 // sequence to finish computes the accepted prefix.
+#include <hip/hip_ext.h>
+
+// One row per workgroup of 512 threads (8 wave64s, 2 per SIMD): the select pass is a
+// chain of short dependent steps, and more waves per SIMD hide their latencies.
+#define BFI_BLOCK 512
 #include "smp_common.h"
 
 namespace bfi {
@@ -36,13 +41,14 @@ struct __align__(16) Smem {
     float hraw[HSLOTS];        // value the streaming pass used (masked, /T)
     float hpen[HSLOTS];        // penalized value (sample.rs:345-375)
     // per-chunk tables (index = chunk)
-    float cm[BLOCK];           // max over the chunk's non-history elements
-    uint32_t carg[BLOCK];      // its first index (greedy)
-    double csum[BLOCK];        // sum of exp(s - cm) over them, or a chunk mass
-    uint32_t cflag[BLOCK];     // ord32 of the largest history value, then the dirty flag
-    uint64_t craw[BLOCK];      // fixed-point streaming-pass terms of the chunk's history ids
-    uint64_t cpen[BLOCK];      // fixed-point penalized terms exp(s - M) of its history ids
-    uint32_t cpre[BLOCK + 1];  // per-chunk candidate prefix (combine)
+    float cm[NCMAX];           // max over the chunk's non-history elements
+    float cxm[NCMAX];          // the chunk's largest masked logit (streaming pass)
+    uint32_t carg[NCMAX];      // its first index (greedy)
+    double csum[NCMAX];        // sum of exp(s - cm) over them, or a chunk mass
+    uint32_t cflag[NCMAX];     // ord32 of the largest history value, then the dirty flag
+    uint64_t craw[NCMAX];      // fixed-point streaming-pass terms of the chunk's history ids
+    uint64_t cpen[NCMAX];      // fixed-point penalized terms exp(s - M) of its history ids
+    uint32_t cpre[NCMAX + 1];  // per-chunk candidate prefix (combine)
     float rf[NWAVE];
     float rf2[NWAVE];
     uint32_t ru[NWAVE];
@@ -52,6 +58,8 @@ struct __align__(16) Smem {
     uint64_t r64b[NWAVE];
     uint32_t misc[8];
 };
+
+constexpr double FIX52 = 4503599627370496.0;  // 2^52: fixed-point scale of the history corrections
 
 // ---- history structures ----------------------------------------------------------------
 
@@ -124,25 +132,57 @@ __device__ __forceinline__ int hist_find(const Smem& sm, uint32_t id) {
 }
 
 // The reference's `HashSet(prev)` (sample.rs:347, 361) plus multiset counts (frequency
-// extension). Returns false when the row has more than HMAX distinct ids.
+// extension). The thread that inserts an id first stores its masked logit in hraw. The id
+// loads and the logit loads of HB entries per thread are each issued together. Returns
+// false when the row has more than HMAX distinct ids (inserts stop there, so the table
+// never fills and every probe sequence ends).
+template <bool BF16>
 __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCtx& C) {
+    constexpr int HB = 4;
     const int tid = threadIdx.x;
     for (int k = tid; k < HSLOTS; k += BLOCK) {
         sm.hkey[k] = HEMPTY;
         sm.hcnt[k] = 0;
     }
     if (tid == 0) sm.misc[MISC_HN] = 0;
-    __syncthreads();
-    if (C.pen_on) {
-        const int64_t H = C.h.size();
-        for (int64_t j = tid; j < H; j += BLOCK) {
-            const uint32_t id = C.h.at(j);
-            if (id >= (uint32_t)a.V) continue;
-            uint32_t k = hslot0(id);
+    const int64_t H = C.pen_on ? C.h.size() : 0;
+    const uint32_t V = (uint32_t)a.V;
+    bool cleared = false;
+    for (int64_t j0 = 0; j0 < H; j0 += (int64_t)HB * BLOCK) {
+        uint32_t id[HB], mw[HB];
+        float x[HB];
+#pragma unroll
+        for (int g = 0; g < HB; g++) {
+            const int64_t j = j0 + g * BLOCK + tid;
+            id[g] = j < H ? C.h.at(j) : HEMPTY;
+        }
+#pragma unroll
+        for (int g = 0; g < HB; g++) {
+            const uint32_t ld = id[g] < V ? id[g] : 0u;
+            if (BF16)
+                x[g] = __uint_as_float((uint32_t)((const uint16_t*)a.logits)[(int64_t)C.row * a.row_stride + ld] << 16);
+            else
+                x[g] = ((const float*)a.logits)[(int64_t)C.row * a.row_stride + ld];
+            mw[g] = C.mrow ? C.mrow[ld >> 5] : 0xFFFFFFFFu;
+        }
+        if (!cleared) {
+            __syncthreads();
+            cleared = true;
+        }
+#pragma unroll
+        for (int g = 0; g < HB; g++) {
+            if (id[g] >= V) continue;
+            if (__hip_atomic_load((BFI_LDS uint32_t*)&sm.misc[MISC_HN], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP) > (uint32_t)HMAX)
+                continue;
+            uint32_t k = hslot0(id[g]);
             for (int probe = 0; probe < HSLOTS; probe++) {
-                const uint32_t prev = lds_cas(&sm.hkey[k], HEMPTY, id);
-                if (prev == HEMPTY || prev == id) {
-                    if (prev == HEMPTY) lds_add(&sm.misc[MISC_HN], 1u);
+                const uint32_t prev = lds_cas(&sm.hkey[k], HEMPTY, id[g]);
+                if (prev == HEMPTY || prev == id[g]) {
+                    if (prev == HEMPTY) {
+                        lds_add(&sm.misc[MISC_HN], 1u);
+                        sm.hraw[k] = ((mw[g] >> (id[g] & 31)) & 1u) ? x[g] : -__builtin_inff();
+                    }
                     lds_add(&sm.hcnt[k], 1u);
                     break;
                 }
@@ -150,8 +190,50 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
             }
         }
     }
+    if (!cleared) __syncthreads();
     __syncthreads();
     return sm.misc[MISC_HN] <= (uint32_t)HMAX;
+}
+
+// Values of the history ids (hash slots): hraw = the un-penalized value x / T, hpen = the
+// penalized one (sample.rs:331-375). Per chunk: the largest hraw (ord32) into cflag, and
+// into craw the terms stream_term the streaming pass added to the chunk's sum for these
+// ids (recomputed with the same expression), in fixed point so that the total does not
+// depend on the order. sm.cxm must hold the chunks' largest masked logits. Returns this
+// thread's max of hpen.
+__device__ __forceinline__ float hist_values(const KArgs& a, Smem& sm, const RowCtx& C) {
+    float hmax = -__builtin_inff();
+    for (int k = threadIdx.x; k < HSLOTS; k += BLOCK) {
+        const uint32_t id = sm.hkey[k];
+        if (id == HEMPTY) continue;
+        const float x = sm.hraw[k];  // masked logit
+        const float vr = raw_value(C, x, true), vp = pen_value(C, x, true, sm.hcnt[k]);
+        sm.hraw[k] = vr;
+        sm.hpen[k] = vp;
+        hmax = fmaxf(hmax, vp);
+        if (vr > -__builtin_inff()) {
+            const uint32_t c = id / (uint32_t)a.chunk;
+            lds_max(&sm.cflag[c], ord32(vr));
+            const float xm = sm.cxm[c];
+            if (!C.greedy && xm > -__builtin_inff()) {
+                const double t = (double)stream_term(C, x, xm);
+                lds_add64(&sm.craw[c], (uint64_t)(t * FIX52));
+            }
+        }
+    }
+    __syncthreads();
+    return hmax;
+}
+
+// Slot for each lane with `pred` in an LDS list whose length is *ctr: one atomic per wave.
+__device__ __forceinline__ uint32_t wave_append(uint32_t* ctr, bool pred) {
+    const uint64_t m = __ballot(pred);
+    if (!m) return 0u;
+    const int leader = __ffsll((unsigned long long)m) - 1;
+    uint32_t base = 0;
+    if (lane_id() == leader) base = lds_add(ctr, (uint32_t)__popcll(m));
+    base = __shfl(base, leader);
+    return base + (uint32_t)__popcll(m & lanes_below());
 }
 
 // Where the penalty membership/counts of an element come from in passes over the row.
@@ -528,7 +610,7 @@ __device__ __forceinline__ int combine_list(const KArgs& a, Smem& sm, const RowC
     for (int j = N + tid; j < n2; j += BLOCK) sm.u.cb.keys[j] = 0ull;
     __syncthreads();
     bitonic_sort_desc(sm.u.cb.keys, n2);
-    BFI_TRACE(a, tb, 3);
+    BFI_TRACE(a, tb, 5);
     // probabilities of the sorted positions: p = expf(s - M) / S (sample.rs:383, 388)
     for (int j = tid; j < N; j += BLOCK) {
         const uint64_t k = sm.u.cb.keys[j];
@@ -607,7 +689,6 @@ __device__ __forceinline__ int combine_list(const KArgs& a, Smem& sm, const RowC
         if (tid == 0) a.t_listed[C.row] = (int32_t)(tc < a.t_cap ? tc : a.t_cap);
     }
 
-    BFI_TRACE(a, tb, 4);
     const double sum = list_sum(sm, nl, wk);
     if (!C.judged) {  // draw (sample.rs:312-323)
         const double r = (double)C.u * sum;
@@ -671,41 +752,43 @@ __device__ __forceinline__ int combine_bounded(const KArgs& a, Smem& sm, const R
         }
         __syncthreads();
         const Cand* cands = a.cands + (int64_t)C.row * nc * CAND_CAP;
-        constexpr int GU = 4;  // loads in flight per thread
+        constexpr int GU = 8;  // candidate loads in flight per thread
         for (uint32_t f0 = tid; f0 < tot; f0 += GU * BLOCK) {
             Cand cd[GU];
+            int lo = 0, hi = nc;  // chunk of f0: largest c with cpre[c] <= f0
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (sm.cpre[mid] <= f0) lo = mid;
+                else hi = mid;
+            }
 #pragma unroll
             for (int g = 0; g < GU; g++) {
                 const uint32_t f = f0 + g * BLOCK;
                 cd[g].idx = 0;
-                cd[g].s = -__builtin_inff();
+                cd[g].x = -__builtin_inff();
                 if (f < tot) {
-                    int lo = 0, hi = nc;  // largest c with cpre[c] <= f
-                    while (hi - lo > 1) {
-                        int mid = (lo + hi) >> 1;
-                        if (sm.cpre[mid] <= f) lo = mid;
-                        else hi = mid;
-                    }
+                    while (sm.cpre[lo + 1] <= f) lo++;  // f only grows
                     cd[g] = cands[(int64_t)lo * CAND_CAP + (f - sm.cpre[lo])];
                 }
             }
 #pragma unroll
             for (int g = 0; g < GU; g++) {
-                if (cd[g].s >= th && cd[g].s > -__builtin_inff() && !(C.pen_on && hist_find(sm, cd[g].idx) >= 0)) {
-                    uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
-                    if (slot < NMAX)
-                        sm.u.cb.keys[slot] = sorted ? key64(cd[g].s, cd[g].idx)
-                                                    : (((uint64_t)(~cd[g].idx) << 32) | ord32(cd[g].s));
-                }
+                const float v = raw_value(C, cd[g].x, true);  // masked logit / T, exact
+                const bool take = v >= th && v > -__builtin_inff() && !(C.pen_on && hist_find(sm, cd[g].idx) >= 0);
+                const uint32_t slot = wave_append(&sm.misc[MISC_N], take);
+                if (take && slot < NMAX)
+                    sm.u.cb.keys[slot] = sorted ? key64(v, cd[g].idx) : (((uint64_t)(~cd[g].idx) << 32) | ord32(v));
             }
         }
         // history ids at their penalized values
-        for (int k = tid; k < HSLOTS; k += BLOCK) {
-            const uint32_t id = sm.hkey[k];
-            const float v = sm.hpen[k];
-            if (id != HEMPTY && v >= th && v > -__builtin_inff()) {
-                uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
-                if (slot < NMAX) sm.u.cb.keys[slot] = sorted ? key64(v, id) : (((uint64_t)(~id) << 32) | ord32(v));
+        if (C.pen_on) {
+            for (int k = tid; k < HSLOTS; k += BLOCK) {
+                const uint32_t id = sm.hkey[k];
+                const float v = sm.hpen[k];
+                const bool take = id != HEMPTY && v >= th && v > -__builtin_inff();
+                const uint32_t slot = wave_append(&sm.misc[MISC_N], take);
+                if (take && slot < NMAX)
+                    sm.u.cb.keys[slot] = sorted ? key64(v, id) : (((uint64_t)(~id) << 32) | ord32(v));
             }
         }
         __syncthreads();
@@ -718,7 +801,7 @@ __device__ __forceinline__ int combine_bounded(const KArgs& a, Smem& sm, const R
             __syncthreads();
         }
         const int N = (int)sm.misc[MISC_N];
-        BFI_TRACE(a, tb, 2);
+        BFI_TRACE(a, tb, 4);
         if (a.trace && tid == 0) a.trace[tb + 6] = ((uint64_t)tot << 32) | (uint32_t)N;
         if (N > NMAX) return CB_RADIX;
         const bool exhaustive = !(th > -__builtin_inff());
@@ -1007,7 +1090,7 @@ __device__ __forceinline__ Sel radix_select(const KArgs& a, Smem& sm, const RowC
             });
             __syncthreads();
         }
-        // scan buckets from the top (o = 0 is bucket nb-1); 4 buckets per thread
+        // scan buckets from the top (o = 0 is bucket nb-1); BPT buckets per thread
         constexpr int BPT = NBUCKET / BLOCK;
         uint64_t lc[BPT], lm[BPT];
         uint64_t rc = 0, rm = 0;
@@ -1315,7 +1398,6 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
 // other elements, so that no subtraction loses precision. Rows with a larger history take
 // whole-row passes with the history tables in global memory.
 
-constexpr double FIX52 = 4503599627370496.0;  // 2^52: fixed-point scale of the corrections
 
 // Every logit is -inf: the reference's weights are NaN and its outcome is deterministic
 // (the min-p fallback argmax, or the last kept id of the draw).
@@ -1366,7 +1448,7 @@ __device__ __forceinline__ bool stats_full(const KArgs& a, Smem& sm, const RowCt
 
 template <bool BF16>
 __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
-    constexpr int VEC = BF16 ? 2 : 4;  // row passes walk 4096-element tiles
+    constexpr int VEC = BF16 ? 2 : 4;  // row passes walk 8192-element tiles
     __shared__ Smem sm;
     const int tid = threadIdx.x;
     // rows grouped per XCD (dispatch is round-robin over the 8 XCDs)
@@ -1393,10 +1475,24 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
         mine.raw_m = -__builtin_inff();
         mine.raw_arg = 0xFFFFFFFFu;
     }
+    // per-chunk accumulators (clear before hist_build's barrier); the history loads are
+    // issued while the chunk results are still in flight
+    if (tid < nc) {
+        sm.cflag[tid] = 0u;
+        sm.craw[tid] = 0ull;
+        sm.cpen[tid] = 0ull;
+    }
+    const bool hashed = hist_build<BF16>(a, sm, C);
+    BFI_TRACE(a, tb, 1);
+    if (tid < nc) {
+        sm.cm[tid] = mine.m;
+        sm.cxm[tid] = mine.raw_m;
+        sm.carg[tid] = mine.arg;
+        sm.csum[tid] = mine.sum;
+    }
+    __syncthreads();
     ArgMax rawmax{-__builtin_inff(), 0xFFFFFFFFu};  // masked, un-penalized (sample.rs:415-422)
     if (track_raw) rawmax = block_argmax(ArgMax{mine.raw_m, mine.raw_arg}, sm.rf, sm.ru);
-
-    const bool hashed = hist_build(a, sm, C);
     const PenSrc H{true, nullptr, nullptr, nullptr};
     const int nw = a.bm_words;
     const uint32_t* gbm = a.row_pen + (int64_t)row * (2 * nw + GDCAP);
@@ -1405,41 +1501,18 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
     double wc = 0.0;  // this thread's chunk: sum of exp(s - M) (hashed rows)
     enum { R_INDEX, R_RADIX };
     int route;
-    if (!hashed) {
+    if (!hashed || (!C.greedy && !C.stream_ok)) {
+        // an oversized history, or a temperature whose streaming values are not usable
         build_row_pen(a, sm, C);
         if (!stats_full<BF16, VEC>(a, sm, C, GT, rawmax, M, S)) return;
         if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 4.0f;
         route = (C.kmode || C.pmode) ? R_RADIX : R_INDEX;
     } else {
-        if (tid < nc) {
-            sm.cm[tid] = mine.m;
-            sm.carg[tid] = mine.arg;
-            sm.csum[tid] = mine.sum;
-            sm.cflag[tid] = 0u;
-            sm.craw[tid] = 0ull;
-            sm.cpen[tid] = 0ull;
-        }
-        __syncthreads();
         // history values: as the streaming pass saw them, and penalized (sample.rs:331-375)
         float hmax = -__builtin_inff();
         uint32_t dirty = 0;
         if (C.pen_on) {
-            for (int k = tid; k < HSLOTS; k += BLOCK) {
-                const uint32_t id = sm.hkey[k];
-                if (id == HEMPTY) continue;
-                float x;
-                if (BF16)
-                    x = __uint_as_float((uint32_t)((const uint16_t*)a.logits)[(int64_t)row * a.row_stride + id] << 16);
-                else
-                    x = ((const float*)a.logits)[(int64_t)row * a.row_stride + id];
-                const bool allowed = !C.mrow || ((C.mrow[id >> 5] >> (id & 31)) & 1u);
-                const float vr = raw_value(C, x, allowed), vp = pen_value(C, x, allowed, sm.hcnt[k]);
-                sm.hraw[k] = vr;
-                sm.hpen[k] = vp;
-                hmax = fmaxf(hmax, vp);
-                if (vr > -__builtin_inff()) lds_max(&sm.cflag[id / (uint32_t)a.chunk], ord32(vr));
-            }
-            __syncthreads();
+            hmax = hist_values(a, sm, C);
             // dirty: a history id holds the chunk's maximum
             if (tid < nc && sm.cflag[tid] != 0u && mine.m > -__builtin_inff() && unord32(sm.cflag[tid]) == mine.m)
                 dirty = 1u;
@@ -1447,7 +1520,6 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
             if (tid < nc) sm.cflag[tid] = dirty;
             __syncthreads();
             if (nd) {
-                BFI_TRACE(a, tb, 5);
                 for (int c = 0; c < nc; c++) {
                     if (!sm.cflag[c]) continue;
                     ArgMax am{-__builtin_inff(), 0xFFFFFFFFu};
@@ -1473,6 +1545,7 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
                 }
             }
         }
+        BFI_TRACE(a, tb, 2);
         if (C.greedy) {  // sample.rs:369-371, 429-439
             ArgMax am{tid < nc ? mine.m : -__builtin_inff(), tid < nc ? mine.arg : 0xFFFFFFFFu};
             if (C.pen_on)
@@ -1487,20 +1560,13 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
             finish_all_masked(a, sm, C, rawmax);
             return;
         }
-        // corrections: out with the streaming terms of the history ids of clean chunks, in
-        // with their penalized terms
+        // corrections: in with the penalized terms of the history ids (their streaming terms
+        // come out of the clean chunks' sums below)
         if (C.pen_on) {
             for (int k = tid; k < HSLOTS; k += BLOCK) {
                 const uint32_t id = sm.hkey[k];
                 if (id == HEMPTY) continue;
                 const uint32_t c = id / (uint32_t)a.chunk;
-                if (!sm.cflag[c]) {
-                    const float mc = sm.cm[c];
-                    if (mc > -__builtin_inff()) {
-                        const double t = (double)__expf(sm.hraw[k] - mc);  // as the streaming pass
-                        lds_add64(&sm.craw[c], (uint64_t)(t * FIX52));
-                    }
-                }
                 const double tp = (double)expf(sm.hpen[k] - M);
                 lds_add64(&sm.cpen[c], (uint64_t)(tp * FIX52));
             }
@@ -1514,7 +1580,7 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
             if (C.pen_on) wc += (double)sm.cpen[tid] / FIX52;
         }
         S = (float)block_sum_d(wc, sm.rd);
-        BFI_TRACE(a, tb, 1);
+        BFI_TRACE(a, tb, 3);
         uint32_t flags = 0;  // some chunk unbounded/overflowed
         if (tid < nc && (mine.ncand == NCAND_UNBOUNDED || mine.ncand == NCAND_OVERFLOW)) flags = 1;
         flags = block_sum_u(flags, sm.ru);
@@ -1541,11 +1607,12 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
         a.t_stats[row * 4 + 0] = M;
         a.t_stats[row * 4 + 1] = S;
     }
+    const bool full = !hashed || !C.stream_ok;  // the global history tables are built
     if (route == R_RADIX) {
-        if (hashed) build_row_pen(a, sm, C);
+        if (!full) build_row_pen(a, sm, C);
         combine_radix<BF16, VEC>(a, sm, C, GT, hashed, M, S, rawmax);
     } else {
-        const bool known = hashed && !C.kmode && !C.pmode && !C.mmode;
+        const bool known = !full && !C.kmode && !C.pmode && !C.mmode;
         combine_index_order_passes<BF16, VEC>(a, sm, C, hashed ? H : GT, hashed, M, S, rawmax, known,
                                               known ? wc / (double)S : 0.0);
     }
@@ -1553,12 +1620,12 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
 
 // ---- launch ----------------------------------------------------------------------------
 
-hipError_t launch_select(const KArgs& a, int bf16, hipStream_t stream) {
+hipError_t launch_select(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const dim3 grid((unsigned)a.n_rows), block(BLOCK);
     if (bf16)
-        hipLaunchKernelGGL((k_select<true>), grid, block, 0, stream, a);
+        hipExtLaunchKernelGGL((k_select<true>), grid, block, 0, stream, start, stop, 0, a);
     else
-        hipLaunchKernelGGL((k_select<false>), grid, block, 0, stream, a);
+        hipExtLaunchKernelGGL((k_select<false>), grid, block, 0, stream, start, stop, 0, a);
     return hipGetLastError();
 }
 

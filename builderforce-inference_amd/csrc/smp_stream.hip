@@ -7,6 +7,8 @@
 // 373-375), and writes per chunk: the max, the f64 sum of exp(s - max), and the elements
 // that can still be kept under the row's top-k or min-p bound. Penalties are left to the
 // select kernel, which corrects the few history ids.
+#include <hip/hip_ext.h>
+
 #include "smp_common.h"
 
 namespace bfi {
@@ -52,69 +54,50 @@ __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
 
     ChunkPart part;
     part.pad = 0;
+    part.pad2 = 0;
     part.raw_m = -__builtin_inff();
     part.raw_arg = 0xFFFFFFFFu;
     part.arg = 0;
-    // mask + temperature, vector by vector as the loads land; running max. The division is
-    // the FMA-corrected one (exact for |x| in [2^-100, 2^100)); a vector in which any lane
-    // of the wave holds another magnitude is divided in IEEE arithmetic instead.
-    const bool track_raw = !C.greedy && C.min_p > 1.0f;
-    const bool fast = !C.greedy && C.fast_div;
-    ArgMax raw{-__builtin_inff(), 0xFFFFFFFFu}, best{-__builtin_inff(), 0xFFFFFFFFu};
+    // pass 1, vector by vector as the loads land: the mask (sample.rs:331-337) in place and
+    // the running max of the masked logits (with its first index for greedy rows and the
+    // min-p fallback, sample.rs:415-422). max(x / T) = max(x) / T for T > 0, so the chunk's
+    // exact maximum takes one division.
+    const bool track_arg = C.greedy || (C.min_p > 1.0f);
+    ArgMax best{-__builtin_inff(), 0xFFFFFFFFu};
     float lm = -__builtin_inff();
 #pragma unroll
     for (int q = 0; q < VEC; q++) {
         const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
-        uint32_t mb = em;
-        if (C.mrow) mb = id0 < c1 ? (C.mrow[id0 >> 5] >> (id0 & 31)) & em : 0u;
-        if (track_raw) {  // masked, un-penalized argmax for the min-p fallback (sample.rs:415-422)
+        if (C.mrow) {
+            const uint32_t mb = id0 < c1 ? (C.mrow[id0 >> 5] >> (id0 & 31)) & em : 0u;
 #pragma unroll
-            for (int e = 0; e < EPV; e++)
-                raw = argmax_merge(raw, ArgMax{((mb >> e) & 1u) ? x[q][e] : -__builtin_inff(), id0 + e});
+            for (int e = 0; e < EPV; e++) x[q][e] = ((mb >> e) & 1u) ? x[q][e] : -__builtin_inff();
         }
-        if (C.greedy) {
+        if (track_arg) {
 #pragma unroll
-            for (int e = 0; e < EPV; e++) {
-                x[q][e] = ((mb >> e) & 1u) ? x[q][e] : -__builtin_inff();
-                best = argmax_merge(best, ArgMax{x[q][e], id0 + e});
-            }
-            continue;
-        }
-        uint32_t erange = 0;  // max of (binary exponent + 99): > 199 outside [2^-100, 2^100)
-        if (fast) {
-#pragma unroll
-            for (int e = 0; e < EPV; e++)
-                erange = max(erange, (uint32_t)(__builtin_amdgcn_frexp_expf(x[q][e]) + 99));
-        }
-        if (fast && __ballot(erange > 199u) == 0) {
-#pragma unroll
-            for (int e = 0; e < EPV; e++) {
-                x[q][e] = ((mb >> e) & 1u) ? div_T_fast(x[q][e], C) : -__builtin_inff();
-                lm = fmaxf(lm, x[q][e]);
-            }
+            for (int e = 0; e < EPV; e++) best = argmax_merge(best, ArgMax{x[q][e], id0 + e});
         } else {
 #pragma unroll
-            for (int e = 0; e < EPV; e++) {
-                x[q][e] = ((mb >> e) & 1u) ? x[q][e] / C.T : -__builtin_inff();
-                lm = fmaxf(lm, x[q][e]);
-            }
+            for (int e = 0; e < EPV; e++) lm = fmaxf(lm, x[q][e]);
         }
     }
     BFI_TRACE(a, tb, 2);
-    if (track_raw) {
-        raw = block_argmax(raw, sm.rf, sm.ru);
-        part.raw_m = raw.v;
-        part.raw_arg = raw.i;
-    }
-    if (C.greedy) {
+    if (track_arg) {
         best = block_argmax(best, sm.rf, sm.ru);
+        lm = best.v;
+        part.raw_arg = best.i;
+    } else {
+        lm = block_max(lm, sm.rf);
+    }
+    part.raw_m = lm;  // the chunk's largest masked logit
+    if (C.greedy) {
         part.m = best.v;
         part.arg = best.i;
         part.sum = 0.0;
         part.ncand = 0;
         part.theta = -__builtin_inff();
     } else {
-        const float mc = block_max(lm, sm.rf);
+        const float mc = div_T(lm, C);  // exact (sample.rs:373-375)
         BFI_TRACE(a, tb, 3);
         part.m = mc;
         const bool kb = C.kmode && C.k <= CAND_CAP;
@@ -125,19 +108,22 @@ __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
             const float lmp = logf(C.min_p);
             th = mc + lmp - (margin + 1e-5f * fabsf(lmp));
         }
-        // one pass: f64 sum of the f32 terms exp(s - max) (the select kernel subtracts
-        // the terms of history ids exactly) and the candidate count at th
+        // pass 2: the f64 sum of the terms stream_term (each vector's EPV terms added in
+        // f32 first) and the count of masked logits at or above the bound th
         double ls = 0.0;
         uint32_t lc = 0;
-        if (mc > -__builtin_inff()) {
+        const float xth = x_bound(C, th);
+        if (lm > -__builtin_inff()) {
 #pragma unroll
-            for (int q = 0; q < VEC; q++)
+            for (int q = 0; q < VEC; q++) {
+                float g = 0.0f;
 #pragma unroll
                 for (int e = 0; e < EPV; e++) {
-                    const float v = x[q][e];
-                    ls += (double)__expf(v - mc);
-                    lc += (v >= th) ? 1u : 0u;
+                    g += stream_term(C, x[q][e], lm);
+                    lc += (x[q][e] >= xth) ? 1u : 0u;
                 }
+                ls += (double)g;
+            }
         }
         uint32_t cnt;
         part.sum = block_sum_du(ls, lc, cnt, sm.rd, sm.ru);
@@ -149,18 +135,15 @@ __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
             part.ncand = NCAND_UNBOUNDED;
             part.theta = __builtin_inff();
         } else {
-            if (!C.mmode) {
-                th = -__builtin_inff();
-                cnt = 0xFFFFFFFFu;
-            }
-            if (kb && cnt > (uint32_t)CAND_CAP) {
-                // smallest power-of-two distance below the chunk max holding k elements,
-                // then bisection toward a tight count
+            uint32_t my = lc;  // this thread's candidates at th
+            if (kb && (!C.mmode || cnt > (uint32_t)CAND_CAP)) {
+                // top-k bound: the smallest power-of-two distance below the chunk max
+                // holding k elements, then bisection toward a tight count
                 float d = 0.25f, lo = 0.0f;
                 uint32_t c = 0;
                 int it = 0;
                 for (; it < 18; it++) {
-                    c = block_sum_u(tile_count_ge<BF16, VEC>(x, mc - d), sm.ru);
+                    c = block_sum_u(tile_count_ge<BF16, VEC>(x, x_bound(C, mc - d)), sm.ru);
                     if (c >= (uint32_t)C.k) break;
                     lo = d;
                     d *= 2.0f;
@@ -172,8 +155,8 @@ __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
                     float hi = d;
                     const uint32_t want = max(2u * (uint32_t)C.k, 64u);
                     for (int j = 0; j < 12 && c > want; j++) {
-                        float mid = 0.5f * (lo + hi);
-                        uint32_t cm = block_sum_u(tile_count_ge<BF16, VEC>(x, mc - mid), sm.ru);
+                        const float mid = 0.5f * (lo + hi);
+                        const uint32_t cm = block_sum_u(tile_count_ge<BF16, VEC>(x, x_bound(C, mc - mid)), sm.ru);
                         if (cm >= (uint32_t)C.k) {
                             hi = mid;
                             c = cm;
@@ -184,14 +167,17 @@ __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
                     tk = mc - hi - margin;
                 }
                 th = C.mmode ? fmaxf(th, tk) : tk;
-                cnt = block_sum_u(tile_count_ge<BF16, VEC>(x, th), sm.ru);
+                my = tile_count_ge<BF16, VEC>(x, x_bound(C, th));
+                cnt = block_sum_u(my, sm.ru);
             }
             part.theta = th;
             if (cnt > (uint32_t)CAND_CAP) {
                 part.ncand = NCAND_OVERFLOW;
             } else {
+                // every element whose exact value is >= th (a few just below may come along)
                 part.ncand = cnt;
-                uint32_t my = tile_count_ge<BF16, VEC>(x, th), tot;
+                const float xw = x_bound(C, th);
+                uint32_t tot;
                 uint32_t o = block_excl_scan<uint32_t>(my, sm.ru, tot);
                 if (my) {
                     Cand* dst = a.cands + ((int64_t)row * a.n_chunks + chunk) * CAND_CAP;
@@ -199,10 +185,9 @@ __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
                     for (int q = 0; q < VEC; q++)
 #pragma unroll
                         for (int e = 0; e < EPV; e++) {
-                            const float v = x[q][e];
-                            if (v >= th && v > -__builtin_inff()) {
+                            if (x[q][e] >= xw && x[q][e] > -__builtin_inff()) {
                                 dst[o].idx = c0 + (uint32_t)(q * BLOCK + tid) * EPV + e;
-                                dst[o].s = v;
+                                dst[o].x = x[q][e];
                                 o++;
                             }
                         }
@@ -216,9 +201,11 @@ __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
 
 // ---- launch ----------------------------------------------------------------------------
 
-hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream) {
+// `start` / `stop` (optional) time the kernel itself (hipExtLaunchKernelGGL records them in
+// the dispatch).
+hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const dim3 grid((unsigned)((int64_t)a.n_rows * a.n_chunks)), block(BLOCK);
-#define BFI_LAUNCH(B, VV) hipLaunchKernelGGL((k_stream<B, VV>), grid, block, 0, stream, a)
+#define BFI_LAUNCH(B, VV) hipExtLaunchKernelGGL((k_stream<B, VV>), grid, block, 0, stream, start, stop, 0, a)
     if (!bf16) {
         if (vec == 8) BFI_LAUNCH(false, 8);
         else if (vec == 4) BFI_LAUNCH(false, 4);
