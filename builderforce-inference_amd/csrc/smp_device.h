@@ -120,6 +120,9 @@ __device__ __forceinline__ uint32_t lds_or(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ uint32_t lds_max(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_max((BFI_LDS uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
+__device__ __forceinline__ uint64_t lds_max64(uint64_t* p, uint64_t v) {
+    return __hip_atomic_fetch_max((BFI_LDS uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 __device__ __forceinline__ uint64_t lds_add64(uint64_t* p, uint64_t v) {
     return __hip_atomic_fetch_add((BFI_LDS uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -157,38 +160,70 @@ __device__ __forceinline__ float key_s(uint64_t k) { return unord32((uint32_t)(k
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// Wave-wide inclusive scans by DPP (no LDS crossbar): Hillis-Steele within each row of 16
+// lanes (row_shr 1, 2, 4, 8), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into
+// rows 2 and 3. Lanes whose DPP source does not exist take the identity. Reductions read
+// the total from lane 63 (a wave-uniform value).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t dpp32(uint32_t identity, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROWMASK, 0xF, false);
+}
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint64_t dpp64(uint64_t identity, uint64_t v) {
+    const uint32_t lo = dpp32<CTRL, ROWMASK>((uint32_t)identity, (uint32_t)v);
+    const uint32_t hi = dpp32<CTRL, ROWMASK>((uint32_t)(identity >> 32), (uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+template <int CTRL, int ROWMASK, typename T>
+__device__ __forceinline__ T dpp_t(T identity, T v) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32/64-bit only");
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, dpp32<CTRL, ROWMASK>(__builtin_bit_cast(uint32_t, identity),
+                                                           __builtin_bit_cast(uint32_t, v)));
+    } else {
+        return __builtin_bit_cast(T, dpp64<CTRL, ROWMASK>(__builtin_bit_cast(uint64_t, identity),
+                                                           __builtin_bit_cast(uint64_t, v)));
+    }
+}
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_scan_incl(T v, T identity, Op op) {
+    v = op(v, dpp_t<0x111, 0xF>(identity, v));  // row_shr:1
+    v = op(v, dpp_t<0x112, 0xF>(identity, v));  // row_shr:2
+    v = op(v, dpp_t<0x114, 0xF>(identity, v));  // row_shr:4
+    v = op(v, dpp_t<0x118, 0xF>(identity, v));  // row_shr:8
+    v = op(v, dpp_t<0x142, 0xA>(identity, v));  // row_bcast:15 -> rows 1, 3
+    v = op(v, dpp_t<0x143, 0xC>(identity, v));  // row_bcast:31 -> rows 2, 3
     return v;
+}
+template <typename T>
+__device__ __forceinline__ T lane63(T v) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    return lane63(wave_scan_incl(v, -__builtin_inff(), [](float x, float y) { return fmaxf(x, y); }));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return lane63(wave_scan_incl(v, 0.0f, [](float x, float y) { return x + y; }));
 }
 __device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return lane63(wave_scan_incl(v, 0.0, [](double x, double y) { return x + y; }));
 }
 __device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return lane63(wave_scan_incl(v, 0u, [](uint32_t x, uint32_t y) { return x + y; }));
 }
 __device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor(v, o));
-    return v;
+    return lane63(wave_scan_incl(v, 0xFFFFFFFFu, [](uint32_t x, uint32_t y) { return x < y ? x : y; }));
 }
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) {
-        uint64_t w = __shfl_xor(v, o);
-        v = w > v ? w : v;
-    }
-    return v;
+    return lane63(wave_scan_incl(v, (uint64_t)0, [](uint64_t x, uint64_t y) { return x > y ? x : y; }));
 }
 
 // Bitonic sort of one key per lane across the wave, descending (lane 0 = largest).
@@ -209,13 +244,7 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
     return key;
 }
 __device__ __forceinline__ double wave_incl_scan_d(double v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        double y = __shfl_up(v, o);
-        if (lane >= o) v += y;
-    }
-    return v;
+    return wave_scan_incl(v, 0.0, [](double x, double y) { return x + y; });
 }
 __device__ __forceinline__ uint64_t lanes_below() { return (1ull << lane_id()) - 1ull; }
 
@@ -326,12 +355,7 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* scr) {
 // result is deterministic for floating-point T.
 template <typename T>
 __device__ __forceinline__ T block_excl_scan(T v, T* scr, T& total) {
-    T x = v;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        T y = __shfl_up(x, o);
-        if (lane_id() >= o) x += y;
-    }
+    const T x = wave_scan_incl(v, (T)0, [](T a, T b) { return a + b; });
     if (lane_id() == WAVE - 1) scr[wave_id()] = x;
     __syncthreads();
     T pre = 0, tot = 0;
@@ -357,13 +381,15 @@ __device__ __forceinline__ ArgMax argmax_merge(ArgMax a, ArgMax b) {
     return a;
 }
 __device__ __forceinline__ ArgMax block_argmax(ArgMax a, float* scrv, uint32_t* scri) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) {
-        ArgMax b;
-        b.v = __shfl_xor(a.v, o);
-        b.i = __shfl_xor(a.i, o);
-        a = argmax_merge(a, b);
-    }
+    // (value, index) packed in 64 bits for the DPP scan; merged with argmax_merge
+    const uint64_t packed = ((uint64_t)__float_as_uint(a.v) << 32) | a.i;
+    const uint64_t ident = ((uint64_t)__float_as_uint(-__builtin_inff()) << 32) | 0xFFFFFFFFu;
+    const uint64_t r64 = lane63(wave_scan_incl(packed, ident, [](uint64_t x, uint64_t y) {
+        const ArgMax m = argmax_merge(ArgMax{__uint_as_float((uint32_t)(x >> 32)), (uint32_t)x},
+                                      ArgMax{__uint_as_float((uint32_t)(y >> 32)), (uint32_t)y});
+        return ((uint64_t)__float_as_uint(m.v) << 32) | m.i;
+    }));
+    a = ArgMax{__uint_as_float((uint32_t)(r64 >> 32)), (uint32_t)r64};
     if (lane_id() == 0) {
         scrv[wave_id()] = a.v;
         scri[wave_id()] = a.i;

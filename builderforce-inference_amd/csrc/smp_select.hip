@@ -20,6 +20,14 @@
 #define BFI_BLOCK 512
 #include "smp_common.h"
 
+// Phase timestamps go to LDS and are written out when the workgroup ends, so that tracing
+// adds no global store (and no wait for one) between phases.
+#undef BFI_TRACE
+#define BFI_TRACE(a, base, i)                                                   \
+    do {                                                                        \
+        if ((a).trace && threadIdx.x == 0) sm.tr[(i)] = wall_clock64();         \
+    } while (0)
+
 namespace bfi {
 
 // ---- shared memory ---------------------------------------------------------------------
@@ -40,6 +48,7 @@ struct __align__(16) Smem {
     uint32_t hcnt[HSLOTS];
     float hraw[HSLOTS];        // value the streaming pass used (masked, /T)
     float hpen[HSLOTS];        // penalized value (sample.rs:345-375)
+    uint16_t hlist[HSLOTS];    // the occupied slots, densely (order of insertion)
     // per-chunk tables (index = chunk)
     float cm[NCMAX];           // max over the chunk's non-history elements
     float cxm[NCMAX];          // the chunk's largest masked logit (streaming pass)
@@ -57,6 +66,19 @@ struct __align__(16) Smem {
     uint64_t r64[NWAVE];
     uint64_t r64b[NWAVE];
     uint32_t misc[8];
+    uint64_t tr[8];  // phase timestamps of this workgroup (diagnostics)
+    // row aggregates built with LDS atomics (integer, so independent of the order)
+    struct {
+        uint64_t gkey;    // greedy: max over (value, index) keys (argmax_key)
+        uint64_t rawkey;  // max (masked logit, index) key: the min-p fallback argmax
+        uint64_t sfix;    // S in 2^-44 fixed point
+        uint32_t mmax;    // ord32 of the largest chunk maximum
+        uint32_t hmax;    // ord32 of the largest penalized history value
+        uint32_t thr;     // ord32 of the largest chunk candidate bound
+        uint32_t flags;   // 1: some chunk has no candidate list
+        uint32_t nd;      // history ids that hold their chunk's maximum
+        uint32_t pad;
+    } ag;
 };
 
 constexpr double FIX52 = 4503599627370496.0;  // 2^52: fixed-point scale of the history corrections
@@ -133,11 +155,12 @@ __device__ __forceinline__ int hist_find(const Smem& sm, uint32_t id) {
 
 // The reference's `HashSet(prev)` (sample.rs:347, 361) plus multiset counts (frequency
 // extension). The thread that inserts an id first stores its masked logit in hraw. The id
-// loads and the logit loads of HB entries per thread are each issued together. Returns
-// false when the row has more than HMAX distinct ids (inserts stop there, so the table
-// never fills and every probe sequence ends).
-template <bool BF16>
-__device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCtx& C) {
+// loads and the logit loads of HB entries per thread are each issued together.
+// `after_clear()` runs between the two barriers (LDS written there is visible on return).
+// Returns false when the row has more than HMAX distinct ids (inserts stop there, so the
+// table never fills and every probe sequence ends).
+template <bool BF16, typename F>
+__device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCtx& C, F after_clear) {
     constexpr int HB = 4;
     const int tid = threadIdx.x;
     for (int k = tid; k < HSLOTS; k += BLOCK) {
@@ -167,6 +190,7 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
         }
         if (!cleared) {
             __syncthreads();
+            after_clear();
             cleared = true;
         }
 #pragma unroll
@@ -180,7 +204,8 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
                 const uint32_t prev = lds_cas(&sm.hkey[k], HEMPTY, id[g]);
                 if (prev == HEMPTY || prev == id[g]) {
                     if (prev == HEMPTY) {
-                        lds_add(&sm.misc[MISC_HN], 1u);
+                        const uint32_t pos = lds_add(&sm.misc[MISC_HN], 1u);  // < HSLOTS: one per key
+                        sm.hlist[pos] = (uint16_t)k;
                         sm.hraw[k] = ((mw[g] >> (id[g] & 31)) & 1u) ? x[g] : -__builtin_inff();
                     }
                     lds_add(&sm.hcnt[k], 1u);
@@ -190,39 +215,80 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
             }
         }
     }
-    if (!cleared) __syncthreads();
+    if (!cleared) {
+        __syncthreads();
+        after_clear();
+    }
     __syncthreads();
     return sm.misc[MISC_HN] <= (uint32_t)HMAX;
 }
 
-// Values of the history ids (hash slots): hraw = the un-penalized value x / T, hpen = the
-// penalized one (sample.rs:331-375). Per chunk: the largest hraw (ord32) into cflag, and
-// into craw the terms stream_term the streaming pass added to the chunk's sum for these
-// ids (recomputed with the same expression), in fixed point so that the total does not
-// depend on the order. sm.cxm must hold the chunks' largest masked logits. Returns this
-// thread's max of hpen.
-__device__ __forceinline__ float hist_values(const KArgs& a, Smem& sm, const RowCtx& C) {
-    float hmax = -__builtin_inff();
-    for (int k = threadIdx.x; k < HSLOTS; k += BLOCK) {
+// Wave-aggregated LDS atomics: the wave reduces first (DPP), then one lane updates LDS.
+// Every lane of the wave must call them.
+__device__ __forceinline__ void wave_lds_max(uint32_t* p, uint32_t v) {
+    v = lane63(wave_scan_incl(v, 0u, [](uint32_t x, uint32_t y) { return x > y ? x : y; }));
+    if (lane_id() == 0) lds_max(p, v);
+}
+__device__ __forceinline__ void wave_lds_max64(uint64_t* p, uint64_t v) {
+    v = lane63(wave_scan_incl(v, (uint64_t)0, [](uint64_t x, uint64_t y) { return x > y ? x : y; }));
+    if (lane_id() == 0) lds_max64(p, v);
+}
+__device__ __forceinline__ void wave_lds_add64(uint64_t* p, uint64_t v) {
+    v = lane63(wave_scan_incl(v, (uint64_t)0, [](uint64_t x, uint64_t y) { return x + y; }));
+    if (lane_id() == 0 && v) lds_add64(p, v);
+}
+__device__ __forceinline__ void wave_lds_add(uint32_t* p, uint32_t v) {
+    v = lane63(wave_scan_incl(v, 0u, [](uint32_t x, uint32_t y) { return x + y; }));
+    if (lane_id() == 0 && v) lds_add(p, v);
+}
+
+// (value, index) as a 64-bit key whose unsigned max is the reference's argmax (largest
+// value, then lowest index; sample.rs:429-439).
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) { return ((uint64_t)ord32(v) << 32) | ~i; }
+__device__ __forceinline__ ArgMax argmax_of_key(uint64_t k) {
+    return k ? ArgMax{unord32((uint32_t)(k >> 32)), ~(uint32_t)k} : ArgMax{-__builtin_inff(), 0xFFFFFFFFu};
+}
+__device__ __forceinline__ float unord_or_ninf(uint32_t o) { return o ? unord32(o) : -__builtin_inff(); }
+
+// Values of the history ids (dense slot list): hraw = the un-penalized value x / T, hpen =
+// the penalized one (sample.rs:331-375). Per chunk, into craw, the terms stream_term the
+// streaming pass added to the chunk's sum for these ids (recomputed with the same
+// expression), in 2^52 fixed point. A history id equal to its chunk's maximum marks the
+// chunk dirty (cflag, ag.nd). Row aggregates: the largest hpen (ag.hmax), or for greedy
+// rows the argmax key (ag.gkey). sm.cm / sm.cxm must hold the chunk results.
+__device__ __forceinline__ void hist_values(const KArgs& a, Smem& sm, const RowCtx& C) {
+    const int nh = (int)sm.misc[MISC_HN];
+    uint64_t gk = 0;
+    uint32_t hm = 0, nd = 0;
+    for (int j = threadIdx.x; j < nh; j += BLOCK) {
+        const int k = sm.hlist[j];
         const uint32_t id = sm.hkey[k];
-        if (id == HEMPTY) continue;
         const float x = sm.hraw[k];  // masked logit
         const float vr = raw_value(C, x, true), vp = pen_value(C, x, true, sm.hcnt[k]);
         sm.hraw[k] = vr;
         sm.hpen[k] = vp;
-        hmax = fmaxf(hmax, vp);
+        const uint64_t key = argmax_key(vp, id);
+        gk = key > gk ? key : gk;
+        hm = max(hm, ord32(vp));
         if (vr > -__builtin_inff()) {
             const uint32_t c = id / (uint32_t)a.chunk;
-            lds_max(&sm.cflag[c], ord32(vr));
             const float xm = sm.cxm[c];
             if (!C.greedy && xm > -__builtin_inff()) {
                 const double t = (double)stream_term(C, x, xm);
                 lds_add64(&sm.craw[c], (uint64_t)(t * FIX52));
             }
+            if (vr == sm.cm[c]) {
+                sm.cflag[c] = 1u;
+                nd++;
+            }
         }
     }
+    if (C.greedy)
+        wave_lds_max64(&sm.ag.gkey, gk);
+    else
+        wave_lds_max(&sm.ag.hmax, hm);
+    wave_lds_add(&sm.ag.nd, nd);
     __syncthreads();
-    return hmax;
 }
 
 // Slot for each lane with `pred` in an LDS list whose length is *ctr: one atomic per wave.
@@ -724,85 +790,132 @@ __device__ __forceinline__ int combine_list(const KArgs& a, Smem& sm, const RowC
 
 
 // Bounded rows (top-k <= CAND_CAP or min-p > 0, every chunk within CAND_CAP).
+// The min-p bound on values: p >= min_p * max p needs s >= M + ln(min_p) (with a margin).
+__device__ __forceinline__ float minp_bound(const RowCtx& C, float M) {
+    if (!C.mmode) return -__builtin_inff();
+    const float lm = logf(C.min_p);
+    return M + lm - (1e-4f + 1e-5f * (fabsf(M) + fabsf(lm)));
+}
+
+// Exclusive prefix of the chunks' candidate counts into sm.cpre (sm.cpre[nc] = total).
+// Rows of at most 64 chunks use wave 0 alone. Needs a barrier before sm.cpre is read.
+__device__ __forceinline__ void chunk_prefix(Smem& sm, int nc, uint32_t myn) {
+    const int tid = threadIdx.x;
+    if (nc <= WAVE) {
+        if (wave_id() == 0) {
+            const uint32_t incl = wave_scan_incl(myn, 0u, [](uint32_t x, uint32_t y) { return x + y; });
+            if (tid < nc) sm.cpre[tid] = incl - myn;
+            const uint32_t tot = lane63(incl);
+            if (tid == 0) sm.cpre[nc] = tot;
+        }
+    } else {
+        uint32_t tot;
+        const uint32_t off = block_excl_scan<uint32_t>(myn, sm.ru, tot);
+        if (tid < nc) sm.cpre[tid] = off;
+        if (tid == 0) sm.cpre[nc] = tot;
+    }
+}
+
+// Candidate loads in flight per thread when gathering a list.
+constexpr int GU = 8;
+
+// The first GU * BLOCK candidates of the flattened chunk lists (prefix sm.cpre): thread t
+// holds f = g * BLOCK + t (g < GU); absent entries read as (0, -inf).
+struct CandBatch {
+    Cand cd[GU];
+};
+__device__ __forceinline__ CandBatch load_cands(const KArgs& a, const Smem& sm, int row, int nc, uint32_t b0) {
+    const uint32_t tot = sm.cpre[nc];
+    const Cand* cands = a.cands + (int64_t)row * nc * CAND_CAP;
+    const uint32_t f0 = b0 + threadIdx.x;
+    CandBatch B;
+    int lo = 0, hi = nc;  // chunk of f0: largest c with cpre[c] <= f0
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (sm.cpre[mid] <= f0) lo = mid;
+        else hi = mid;
+    }
+#pragma unroll
+    for (int g = 0; g < GU; g++) {
+        const uint32_t f = f0 + g * BLOCK;
+        B.cd[g].idx = 0;
+        B.cd[g].x = -__builtin_inff();
+        if (f < tot) {
+            while (sm.cpre[lo + 1] <= f) lo++;  // f only grows
+            B.cd[g] = cands[(int64_t)lo * CAND_CAP + (f - sm.cpre[lo])];
+        }
+    }
+    return B;
+}
+
+// Appends the non-history candidates of B whose exact value is >= th to the list. Every
+// thread of the block calls it (wave_append).
+__device__ __forceinline__ void append_cands(Smem& sm, const RowCtx& C, const CandBatch& B, float th, bool sorted) {
+#pragma unroll
+    for (int g = 0; g < GU; g++) {
+        const float v = raw_value(C, B.cd[g].x, true);  // masked logit / T, exact
+        const bool take = v >= th && v > -__builtin_inff() && !(C.pen_on && hist_find(sm, B.cd[g].idx) >= 0);
+        const uint32_t slot = wave_append(&sm.misc[MISC_N], take);
+        if (take && slot < NMAX)
+            sm.u.cb.keys[slot] = sorted ? key64(v, B.cd[g].idx) : (((uint64_t)(~B.cd[g].idx) << 32) | ord32(v));
+    }
+}
+
+// Appends the history ids whose penalized value is >= th. Every thread calls it.
+__device__ __forceinline__ void append_hist(Smem& sm, const RowCtx& C, float th, bool sorted) {
+    if (!C.pen_on) return;
+    const int nh = (int)sm.misc[MISC_HN];
+    for (int j0 = 0; j0 < nh; j0 += BLOCK) {  // uniform trip count: wave_append below
+        const int j = j0 + threadIdx.x;
+        const int k = j < nh ? sm.hlist[j] : 0;
+        const uint32_t id = sm.hkey[k];
+        const float v = sm.hpen[k];
+        const bool take = j < nh && v >= th && v > -__builtin_inff();
+        const uint32_t slot = wave_append(&sm.misc[MISC_N], take);
+        if (take && slot < NMAX) sm.u.cb.keys[slot] = sorted ? key64(v, id) : (((uint64_t)(~id) << 32) | ord32(v));
+    }
+}
+
+// Candidates chunk c contributes to a list complete above th (the repair pass re-reads the
+// chunks whose own bound lies above th).
+__device__ __forceinline__ uint32_t chunk_take(const ChunkPart& mine, float th) {
+    return (mine.theta <= th && mine.m >= th) ? mine.ncand : 0u;
+}
+
+// `th_raw`: every non-history element >= th_raw is some chunk's candidate (the largest chunk
+// bound). `list_ready`: the first pass's list (complete above max(th_raw, min-p bound)) is
+// already in sm.u.cb.keys with its length in MISC_N.
 template <bool BF16, int VEC>
 __device__ __forceinline__ int combine_bounded(const KArgs& a, Smem& sm, const RowCtx& C, const ChunkPart& mine,
-                                               float M, float S, ArgMax rawmax, int64_t tb) {
+                                               float M, float S, ArgMax rawmax, float th_raw, bool list_ready,
+                                               int64_t tb) {
     const int tid = threadIdx.x;
     const int nc = a.n_chunks;
     const bool sorted = C.kmode || C.pmode;  // else min-p only: index order (sample.rs:411-414)
-    // every non-history element >= th_raw is some chunk's candidate
-    const float th_raw = block_max(tid < nc ? mine.theta : -__builtin_inff(), sm.rf);
-    float th_m = -__builtin_inff();
-    if (C.mmode) {  // p >= min_p * max p needs s >= M + ln(min_p)
-        const float lm = logf(C.min_p);
-        th_m = M + lm - (1e-4f + 1e-5f * (fabsf(M) + fabsf(lm)));
-    }
+    const float th_m = minp_bound(C, M);
     float th = fmaxf(th_raw, th_m);
     for (int pass = 0; pass < 2; pass++) {
         // ---- the list: complete above th
-        // chunks whose own bound is above th (only in the repair pass) are re-read
-        const bool from_cands = tid < nc && mine.theta <= th && mine.m >= th;
-        uint32_t myn = from_cands ? mine.ncand : 0u;
-        uint32_t tot;
-        uint32_t off = block_excl_scan<uint32_t>(myn, sm.ru, tot);
-        if (tid < nc) sm.cpre[tid] = off;
-        if (tid == 0) {
-            sm.cpre[nc] = tot;
-            sm.misc[MISC_N] = 0;
-        }
-        __syncthreads();
-        const Cand* cands = a.cands + (int64_t)C.row * nc * CAND_CAP;
-        constexpr int GU = 8;  // candidate loads in flight per thread
-        for (uint32_t f0 = tid; f0 < tot; f0 += GU * BLOCK) {
-            Cand cd[GU];
-            int lo = 0, hi = nc;  // chunk of f0: largest c with cpre[c] <= f0
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (sm.cpre[mid] <= f0) lo = mid;
-                else hi = mid;
-            }
-#pragma unroll
-            for (int g = 0; g < GU; g++) {
-                const uint32_t f = f0 + g * BLOCK;
-                cd[g].idx = 0;
-                cd[g].x = -__builtin_inff();
-                if (f < tot) {
-                    while (sm.cpre[lo + 1] <= f) lo++;  // f only grows
-                    cd[g] = cands[(int64_t)lo * CAND_CAP + (f - sm.cpre[lo])];
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < GU; g++) {
-                const float v = raw_value(C, cd[g].x, true);  // masked logit / T, exact
-                const bool take = v >= th && v > -__builtin_inff() && !(C.pen_on && hist_find(sm, cd[g].idx) >= 0);
-                const uint32_t slot = wave_append(&sm.misc[MISC_N], take);
-                if (take && slot < NMAX)
-                    sm.u.cb.keys[slot] = sorted ? key64(v, cd[g].idx) : (((uint64_t)(~cd[g].idx) << 32) | ord32(v));
-            }
-        }
-        // history ids at their penalized values
-        if (C.pen_on) {
-            for (int k = tid; k < HSLOTS; k += BLOCK) {
-                const uint32_t id = sm.hkey[k];
-                const float v = sm.hpen[k];
-                const bool take = id != HEMPTY && v >= th && v > -__builtin_inff();
-                const uint32_t slot = wave_append(&sm.misc[MISC_N], take);
-                if (take && slot < NMAX)
-                    sm.u.cb.keys[slot] = sorted ? key64(v, id) : (((uint64_t)(~id) << 32) | ord32(v));
-            }
-        }
-        __syncthreads();
-        // re-read the chunks whose candidates stop above th (repair pass)
-        if (pass) {
-            for (int c = 0; c < nc; c++) {
-                const float tc = sm.cm[c] >= th ? a.parts[(int64_t)C.row * nc + c].theta : -__builtin_inff();
-                if (tc > th) rescan_collect<BF16, VEC>(a, sm, C, (uint32_t)c, th, sorted);
-            }
+        if (!(pass == 0 && list_ready)) {
+            chunk_prefix(sm, nc, tid < nc ? chunk_take(mine, th) : 0u);
+            if (tid == 0) sm.misc[MISC_N] = 0;
             __syncthreads();
+            for (uint32_t b0 = 0; b0 < sm.cpre[nc]; b0 += GU * BLOCK)  // uniform trip count
+                append_cands(sm, C, load_cands(a, sm, C.row, nc, b0), th, sorted);
+            append_hist(sm, C, th, sorted);
+            __syncthreads();
+            // re-read the chunks whose candidates stop above th (repair pass)
+            if (pass) {
+                for (int c = 0; c < nc; c++) {
+                    const float tc = sm.cm[c] >= th ? a.parts[(int64_t)C.row * nc + c].theta : -__builtin_inff();
+                    if (tc > th) rescan_collect<BF16, VEC>(a, sm, C, (uint32_t)c, th, sorted);
+                }
+                __syncthreads();
+            }
         }
         const int N = (int)sm.misc[MISC_N];
         BFI_TRACE(a, tb, 4);
-        if (a.trace && tid == 0) a.trace[tb + 6] = ((uint64_t)tot << 32) | (uint32_t)N;
+        if (a.trace && tid == 0) sm.tr[6] = ((uint64_t)sm.cpre[nc] << 32) | (uint32_t)N;
         if (N > NMAX) return CB_RADIX;
         const bool exhaustive = !(th > -__builtin_inff());
         const bool minp_complete = th <= th_m;
@@ -1446,21 +1559,26 @@ __device__ __forceinline__ bool stats_full(const KArgs& a, Smem& sm, const RowCt
     return true;
 }
 
-template <bool BF16>
-__global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
-    constexpr int VEC = BF16 ? 2 : 4;  // row passes walk 8192-element tiles
-    __shared__ Smem sm;
-    const int tid = threadIdx.x;
-    // rows grouped per XCD (dispatch is round-robin over the 8 XCDs)
+// Row handled by this workgroup: rows grouped per XCD (dispatch is round-robin over the 8
+// XCDs).
+__device__ __forceinline__ int select_row_id() {
     const uint32_t G = gridDim.x, bid = blockIdx.x;
     const uint32_t q8 = G / 8, r8 = G % 8, xcd = bid % 8, slot = bid / 8;
-    const int row = (int)(xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot);
-    const int64_t tb = ((int64_t)a.n_rows * a.n_chunks + row) * 8;
+    return (int)(xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot);
+}
+
+template <bool BF16>
+__device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
+    constexpr int VEC = BF16 ? 2 : 4;  // row passes walk 8192-element tiles
+    const int tid = threadIdx.x;
+    const int row = select_row_id();
+    const int64_t tb = 0;
     BFI_TRACE(a, tb, 0);
     if (row >= a.n_rows) return;
     const RowCtx C = make_ctx(a, row);
     if (!C.active) return;
     const bool track_raw = !C.greedy && C.min_p > 1.0f;
+    const bool cand_row = !C.greedy && (C.kmode || C.pmode || C.mmode);  // may have candidate lists
 
     const int nc = a.n_chunks;
     ChunkPart mine;
@@ -1475,30 +1593,56 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
         mine.raw_m = -__builtin_inff();
         mine.raw_arg = 0xFFFFFFFFu;
     }
-    // per-chunk accumulators (clear before hist_build's barrier); the history loads are
-    // issued while the chunk results are still in flight
+    // ---- A: history hash; chunk results into LDS and the row aggregates (one pair of
+    // barriers; the history loads are issued while the chunk results are in flight)
     if (tid < nc) {
         sm.cflag[tid] = 0u;
         sm.craw[tid] = 0ull;
         sm.cpen[tid] = 0ull;
     }
-    const bool hashed = hist_build<BF16>(a, sm, C);
-    BFI_TRACE(a, tb, 1);
-    if (tid < nc) {
-        sm.cm[tid] = mine.m;
-        sm.cxm[tid] = mine.raw_m;
-        sm.carg[tid] = mine.arg;
-        sm.csum[tid] = mine.sum;
+    if (tid == 0) {
+        sm.ag.gkey = 0ull;
+        sm.ag.rawkey = 0ull;
+        sm.ag.sfix = 0ull;
+        sm.ag.mmax = 0u;
+        sm.ag.hmax = 0u;
+        sm.ag.thr = 0u;
+        sm.ag.flags = 0u;
+        sm.ag.nd = 0u;
     }
-    __syncthreads();
-    ArgMax rawmax{-__builtin_inff(), 0xFFFFFFFFu};  // masked, un-penalized (sample.rs:415-422)
-    if (track_raw) rawmax = block_argmax(ArgMax{mine.raw_m, mine.raw_arg}, sm.rf, sm.ru);
+    const bool hashed = hist_build<BF16>(a, sm, C, [&]() {
+        if (tid < nc) {
+            sm.cm[tid] = mine.m;
+            sm.cxm[tid] = mine.raw_m;
+            sm.carg[tid] = mine.arg;
+            sm.csum[tid] = mine.sum;
+        }
+        if (wave_id() * WAVE < nc) {  // waves holding chunks
+            const bool in = tid < nc;
+            wave_lds_max(&sm.ag.mmax, in && mine.m > -__builtin_inff() ? ord32(mine.m) : 0u);
+            wave_lds_max(&sm.ag.thr, in ? ord32(mine.theta) : 0u);
+            wave_lds_add(&sm.ag.flags, in && (mine.ncand == NCAND_UNBOUNDED || mine.ncand == NCAND_OVERFLOW));
+            if (C.greedy) wave_lds_max64(&sm.ag.gkey, in ? argmax_key(mine.m, mine.arg) : 0ull);
+            if (track_raw) wave_lds_max64(&sm.ag.rawkey, in ? argmax_key(mine.raw_m, mine.raw_arg) : 0ull);
+        }
+        // prefix over every chunk's candidate list (the first pass filters them later)
+        if (cand_row) chunk_prefix(sm, nc, tid < nc && mine.ncand <= (uint32_t)CAND_CAP ? mine.ncand : 0u);
+        if (tid == 0) sm.misc[MISC_N] = 0;
+    });
+    BFI_TRACE(a, tb, 1);
+    // bounded rows: the first candidate loads go out now and land during the history work
+    const bool unfiltered = !C.kmode && !C.pmode && !C.mmode;
+    const bool bounded = cand_row && hashed && C.stream_ok && sm.ag.flags == 0u;
+    CandBatch first;
+    if (bounded) first = load_cands(a, sm, row, nc, 0);
+    // masked, un-penalized argmax (min-p fallback, sample.rs:415-422)
+    const ArgMax rawmax = track_raw ? argmax_of_key(sm.ag.rawkey) : ArgMax{-__builtin_inff(), 0xFFFFFFFFu};
     const PenSrc H{true, nullptr, nullptr, nullptr};
     const int nw = a.bm_words;
     const uint32_t* gbm = a.row_pen + (int64_t)row * (2 * nw + GDCAP);
     const PenSrc GT{false, gbm, gbm + nw, gbm + 2 * nw};
     float M, S;
-    double wc = 0.0;  // this thread's chunk: sum of exp(s - M) (hashed rows)
+    double wc = 0.0;  // this thread's chunk: sum of exp(s - M) over it (hashed rows)
     enum { R_INDEX, R_RADIX };
     int route;
     if (!hashed || (!C.greedy && !C.stream_ok)) {
@@ -1508,18 +1652,14 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
         if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 4.0f;
         route = (C.kmode || C.pmode) ? R_RADIX : R_INDEX;
     } else {
-        // history values: as the streaming pass saw them, and penalized (sample.rs:331-375)
-        float hmax = -__builtin_inff();
+        // ---- B: history values (sample.rs:331-375) and the streaming terms they replace
         uint32_t dirty = 0;
         if (C.pen_on) {
-            hmax = hist_values(a, sm, C);
-            // dirty: a history id holds the chunk's maximum
-            if (tid < nc && sm.cflag[tid] != 0u && mine.m > -__builtin_inff() && unord32(sm.cflag[tid]) == mine.m)
-                dirty = 1u;
-            const uint32_t nd = block_sum_u(dirty, sm.ru);
-            if (tid < nc) sm.cflag[tid] = dirty;
-            __syncthreads();
-            if (nd) {
+            hist_values(a, sm, C);
+            if (sm.ag.nd) {
+                // rare: a chunk whose maximum is a history id; re-read it for the max and
+                // sum of its other elements, then refresh the aggregates
+                dirty = tid < nc ? sm.cflag[tid] : 0u;
                 for (int c = 0; c < nc; c++) {
                     if (!sm.cflag[c]) continue;
                     ArgMax am{-__builtin_inff(), 0xFFFFFFFFu};
@@ -1535,6 +1675,8 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
                         sm.cm[c] = am.v;
                         sm.carg[c] = am.i;
                         sm.csum[c] = ls;
+                        sm.ag.mmax = 0u;
+                        if (C.greedy) sm.ag.gkey = 0ull;
                     }
                 }
                 __syncthreads();
@@ -1543,65 +1685,73 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
                     mine.arg = sm.carg[tid];
                     mine.sum = sm.csum[tid];
                 }
+                const bool in = tid < nc;
+                wave_lds_max(&sm.ag.mmax, in && mine.m > -__builtin_inff() ? ord32(mine.m) : 0u);
+                if (C.greedy) {
+                    uint64_t gk = in ? argmax_key(mine.m, mine.arg) : 0ull;
+                    for (int j = tid; j < (int)sm.misc[MISC_HN]; j += BLOCK) {
+                        const int k = sm.hlist[j];
+                        const uint64_t key = argmax_key(sm.hpen[k], sm.hkey[k]);
+                        gk = key > gk ? key : gk;
+                    }
+                    wave_lds_max64(&sm.ag.gkey, gk);
+                }
+                __syncthreads();
             }
         }
         BFI_TRACE(a, tb, 2);
         if (C.greedy) {  // sample.rs:369-371, 429-439
-            ArgMax am{tid < nc ? mine.m : -__builtin_inff(), tid < nc ? mine.arg : 0xFFFFFFFFu};
-            if (C.pen_on)
-                for (int k = tid; k < HSLOTS; k += BLOCK)
-                    if (sm.hkey[k] != HEMPTY) am = argmax_merge(am, ArgMax{sm.hpen[k], sm.hkey[k]});
-            am = block_argmax(am, sm.rf, sm.ru);
+            const ArgMax am = argmax_of_key(sm.ag.gkey);
             finish_token(a, sm, C, am.v > -__builtin_inff() ? am.i : 0u);
             return;
         }
-        M = block_max(fmaxf(tid < nc ? mine.m : -__builtin_inff(), hmax), sm.rf);
+        M = fmaxf(unord_or_ninf(sm.ag.mmax), unord_or_ninf(sm.ag.hmax));
         if (!(M > -__builtin_inff())) {
             finish_all_masked(a, sm, C, rawmax);
             return;
         }
-        // corrections: in with the penalized terms of the history ids (their streaming terms
-        // come out of the clean chunks' sums below)
+        // ---- C: S (penalized terms of the history ids + the chunks' corrected sums, in
+        // 2^-44 fixed point) and, for bounded rows, the candidate prefix of the first pass
+        constexpr double FIX44 = 17592186044416.0;
+        uint64_t sf = 0;  // this thread's share of S, fixed point
         if (C.pen_on) {
-            for (int k = tid; k < HSLOTS; k += BLOCK) {
-                const uint32_t id = sm.hkey[k];
-                if (id == HEMPTY) continue;
-                const uint32_t c = id / (uint32_t)a.chunk;
+            for (int j = tid; j < (int)sm.misc[MISC_HN]; j += BLOCK) {
+                const int k = sm.hlist[j];
+                const uint32_t c = sm.hkey[k] / (uint32_t)a.chunk;
                 const double tp = (double)expf(sm.hpen[k] - M);
                 lds_add64(&sm.cpen[c], (uint64_t)(tp * FIX52));
+                sf += (uint64_t)(tp * FIX44);
             }
-            __syncthreads();
         }
-        if (tid < nc) {
-            if (mine.m > -__builtin_inff()) {
-                const double rc = mine.sum - (C.pen_on && !dirty ? (double)sm.craw[tid] / FIX52 : 0.0);
-                wc = rc * (double)expf(mine.m - M);
-            }
-            if (C.pen_on) wc += (double)sm.cpen[tid] / FIX52;
+        if (tid < nc && mine.m > -__builtin_inff()) {
+            const double rc = mine.sum - (C.pen_on && !dirty ? (double)sm.craw[tid] / FIX52 : 0.0);
+            wc = rc * (double)expf(mine.m - M);
+            sf += (uint64_t)(wc * FIX44);
         }
-        S = (float)block_sum_d(wc, sm.rd);
+        wave_lds_add64(&sm.ag.sfix, sf);
+        const float th_raw = unord_or_ninf(sm.ag.thr);
+        if (bounded) {  // the first pass's list: complete above max(th_raw, min-p bound)
+            const float th = fmaxf(th_raw, minp_bound(C, M));
+            const bool sorted = C.kmode || C.pmode;
+            append_cands(sm, C, first, th, sorted);
+            for (uint32_t b0 = GU * BLOCK; b0 < sm.cpre[nc]; b0 += GU * BLOCK)  // uniform trip count
+                append_cands(sm, C, load_cands(a, sm, row, nc, b0), th, sorted);
+            append_hist(sm, C, th, sorted);
+        }
+        __syncthreads();
+        S = (float)((double)sm.ag.sfix / FIX44);
+        if (tid < nc && C.pen_on) wc += (double)sm.cpen[tid] / FIX52;
         BFI_TRACE(a, tb, 3);
-        uint32_t flags = 0;  // some chunk unbounded/overflowed
-        if (tid < nc && (mine.ncand == NCAND_UNBOUNDED || mine.ncand == NCAND_OVERFLOW)) flags = 1;
-        flags = block_sum_u(flags, sm.ru);
-        if (!C.kmode && !C.pmode && !C.mmode) {
-            if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 2.0f;
-            route = R_INDEX;
-        } else {
-            if (flags == 0) {
-                if (a.t_stats && tid == 0) {
-                    a.t_stats[row * 4 + 0] = M;
-                    a.t_stats[row * 4 + 1] = S;
-                    a.t_stats[row * 4 + 3] = 1.0f;
-                }
-                if (combine_bounded<BF16, VEC>(a, sm, C, mine, M, S, rawmax, tb) == CB_DONE) {
-                    BFI_TRACE(a, tb, 7);
-                    return;
-                }
-            }
-            if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 3.0f;
-            route = (C.kmode || C.pmode) ? R_RADIX : R_INDEX;
+        if (a.t_stats && tid == 0) {
+            a.t_stats[row * 4 + 0] = M;
+            a.t_stats[row * 4 + 1] = S;
+            a.t_stats[row * 4 + 3] = unfiltered ? 2.0f : (bounded ? 1.0f : 3.0f);
         }
+        if (bounded) {
+            if (combine_bounded<BF16, VEC>(a, sm, C, mine, M, S, rawmax, th_raw, true, tb) == CB_DONE) return;
+            if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 3.0f;
+        }
+        route = (C.kmode || C.pmode) ? R_RADIX : R_INDEX;
     }
     if (a.t_stats && tid == 0) {
         a.t_stats[row * 4 + 0] = M;
@@ -1615,6 +1765,20 @@ __global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
         const bool known = !full && !C.kmode && !C.pmode && !C.mmode;
         combine_index_order_passes<BF16, VEC>(a, sm, C, hashed ? H : GT, hashed, M, S, rawmax, known,
                                               known ? wc / (double)S : 0.0);
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
+    __shared__ Smem sm;
+    if (a.trace && threadIdx.x == 0)
+        for (int i = 0; i < 8; i++) sm.tr[i] = 0;
+    select_row<BF16>(a, sm);
+    const int row = select_row_id();
+    if (a.trace && threadIdx.x == 0 && row < a.n_rows) {
+        sm.tr[7] = wall_clock64();
+        uint64_t* t = a.trace + ((int64_t)a.n_rows * a.n_chunks + row) * 8;
+        for (int i = 0; i < 8; i++) t[i] = sm.tr[i];
     }
 }
 
