@@ -226,21 +226,66 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return lane63(wave_scan_incl(v, (uint64_t)0, [](uint64_t x, uint64_t y) { return x > y ? x : y; }));
 }
 
+// v of lane (lane ^ S), without the LDS crossbar: DPP quad_perm for 1 and 2, row_shl/shr:4
+// for 4, row_ror:8 for 8, and gfx950's v_permlane16/32_swap for 16 and 32. All lanes must
+// be active.
+template <int S>
+__device__ __forceinline__ uint32_t wave_xor32(uint32_t v) {
+    const int lane = lane_id();
+    if constexpr (S == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (S == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (S == 4) {
+        const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);  // row_shl:4
+        const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+        return (lane & 4) ? dn : up;
+    } else if constexpr (S == 8) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    } else if constexpr (S == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? r[0] : r[1];
+    } else {
+        static_assert(S == 32, "xor distance 1..32");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32) ? r[0] : r[1];
+    }
+}
+template <int S>
+__device__ __forceinline__ uint64_t wave_xor64(uint64_t v) {
+    return ((uint64_t)wave_xor32<S>((uint32_t)(v >> 32)) << 32) | wave_xor32<S>((uint32_t)v);
+}
+
+// One compare-exchange stage of a bitonic network over keys held one per lane (position
+// j): the partner is j ^ S; `desc` = this position's block sorts descending.
+template <int S>
+__device__ __forceinline__ uint64_t bitonic_step(uint64_t key, int j, bool desc) {
+    const uint64_t other = wave_xor64<S>(key);
+    const bool take_max = ((j & S) == 0) == desc;
+    const uint64_t mx = other > key ? other : key, mn = other > key ? key : other;
+    return take_max ? mx : mn;
+}
+// The stages of a bitonic merge of blocks of `size` with strides 32 .. 1 (in-wave part).
+template <int TOP>
+__device__ __forceinline__ uint64_t bitonic_wave_strides(uint64_t key, int j, bool desc) {
+    if constexpr (TOP >= 32) key = bitonic_step<32>(key, j, desc);
+    if constexpr (TOP >= 16) key = bitonic_step<16>(key, j, desc);
+    if constexpr (TOP >= 8) key = bitonic_step<8>(key, j, desc);
+    if constexpr (TOP >= 4) key = bitonic_step<4>(key, j, desc);
+    if constexpr (TOP >= 2) key = bitonic_step<2>(key, j, desc);
+    key = bitonic_step<1>(key, j, desc);
+    return key;
+}
+
 // Bitonic sort of one key per lane across the wave, descending (lane 0 = largest).
 __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
     const int lane = lane_id();
-#pragma unroll
-    for (int size = 2; size <= WAVE; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const uint64_t other = __shfl_xor(key, stride);
-            const bool desc = (lane & size) == 0 || size == WAVE;
-            const bool lower = (lane & stride) == 0;
-            const bool take_max = lower == desc;
-            const uint64_t mx = other > key ? other : key, mn = other > key ? key : other;
-            key = take_max ? mx : mn;
-        }
-    }
+    key = bitonic_wave_strides<1>(key, lane, (lane & 2) == 0);
+    key = bitonic_wave_strides<2>(key, lane, (lane & 4) == 0);
+    key = bitonic_wave_strides<4>(key, lane, (lane & 8) == 0);
+    key = bitonic_wave_strides<8>(key, lane, (lane & 16) == 0);
+    key = bitonic_wave_strides<16>(key, lane, (lane & 32) == 0);
+    key = bitonic_wave_strides<32>(key, lane, true);
     return key;
 }
 __device__ __forceinline__ double wave_incl_scan_d(double v) {

@@ -494,22 +494,80 @@ __device__ __forceinline__ double list_sum(Smem& sm, int n, W w) {
     return block_sum_d(run, sm.rd);
 }
 
+// Orders LDS writes of this wave before its later LDS reads (lanes of one wave only).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Bitonic sort of n (a power of two, <= 2 * NMAX) 64-bit keys in LDS, descending. A stage
+// with stride <= 64 touches only its wave's own 128-key segments, so between two such stages
+// a wave-level sync suffices; block barriers separate the others.
 __device__ __forceinline__ void bitonic_sort_desc(uint64_t* k, int n) {
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             for (int i = threadIdx.x; i < n / 2; i += BLOCK) {
-                int lo = 2 * i - (i & (stride - 1));
-                int hi = lo + stride;
-                bool desc = (lo & size) == 0;
-                uint64_t x = k[lo], y = k[hi];
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool desc = (lo & size) == 0;
+                const uint64_t x = k[lo], y = k[hi];
                 if ((x < y) == desc) {
                     k[lo] = y;
                     k[hi] = x;
                 }
             }
-            __syncthreads();
+            const int next = stride > 1 ? stride >> 1 : size;  // the next stage's stride
+            const bool last = stride == 1 && size == n;
+            if (!last && stride <= WAVE && next <= WAVE)
+                wave_lds_sync();
+            else
+                __syncthreads();
         }
     }
+}
+
+// Sorts the N keys of the list (padding to a power of two with 0, which sorts last).
+__device__ __forceinline__ void sort_list(Smem& sm, int N) {
+    int n2 = 64;
+    while (n2 < N) n2 <<= 1;
+    for (int j = N + threadIdx.x; j < n2; j += BLOCK) sm.u.cb.keys[j] = 0ull;
+    __syncthreads();
+    bitonic_sort_desc(sm.u.cb.keys, n2);
+}
+
+// Sorts the list's N keys (64 < N <= BLOCK) descending into sm.u.cb.keys[0, N): one key per
+// thread in registers; strides below 64 exchange within the wave (DPP / permlane), larger
+// ones through two alternating LDS buffers (one barrier each).
+__device__ __forceinline__ void sort_list_regs(Smem& sm, int N) {
+    static_assert(3 * BLOCK <= NMAX, "exchange buffers");
+    const int j = threadIdx.x;
+    int n = 128;
+    while (n < N) n <<= 1;
+    uint64_t key = j < N ? sm.u.cb.keys[j] : 0ull;  // padding (0) sorts last
+    key = bitonic_wave_strides<1>(key, j, (j & 2) == 0);
+    key = bitonic_wave_strides<2>(key, j, (j & 4) == 0);
+    key = bitonic_wave_strides<4>(key, j, (j & 8) == 0);
+    key = bitonic_wave_strides<8>(key, j, (j & 16) == 0);
+    key = bitonic_wave_strides<16>(key, j, (j & 32) == 0);
+    key = bitonic_wave_strides<32>(key, j, (j & 64) == 0);
+    int buf = 0;
+    for (int size = 128; size <= n; size <<= 1) {
+        const bool desc = (j & size) == 0;
+        for (int stride = size >> 1; stride >= WAVE; stride >>= 1) {
+            uint64_t* b = sm.u.cb.keys + BLOCK * (1 + buf);
+            b[j] = key;
+            __syncthreads();
+            const uint64_t other = b[j ^ stride];
+            buf ^= 1;
+            const bool take_max = ((j & stride) == 0) == desc;
+            const uint64_t mx = other > key ? other : key, mn = other > key ? key : other;
+            key = take_max ? mx : mn;
+        }
+        key = bitonic_wave_strides<32>(key, j, desc);
+    }
+    if (j < N) sm.u.cb.keys[j] = key;
+    __syncthreads();
 }
 
 // ---- combine: bounded candidates -------------------------------------------------------
@@ -529,26 +587,88 @@ __device__ __forceinline__ bool resolve_L(int64_t Lk, int64_t Lp, int64_t Lm, in
     return L != L_UNKNOWN && (L <= N || exhaustive);
 }
 
-// N <= 64 candidates: wave 0 does everything in registers with shuffles and ballots; the
-// other waves wait for the result. Returns false when the list does not decide the cut.
+// List positions held by wave 0 in registers: position j = E * lane + e (e < E).
+struct WPos {
+    int64_t pos;  // -1 when absent
+    int lane, e;
+};
+// First position (in list order) whose pred is set.
+template <int E>
+__device__ __forceinline__ WPos wave_first(const bool (&pred)[E]) {
+    int fe = E;
+#pragma unroll
+    for (int e = E - 1; e >= 0; e--)
+        if (pred[e]) fe = e;
+    const uint64_t hit = __ballot(fe < E);
+    if (!hit) return WPos{-1, 0, 0};
+    const int l0 = __ffsll((unsigned long long)hit) - 1;
+    const int e0 = __builtin_amdgcn_readlane(fe, l0);
+    return WPos{(int64_t)E * l0 + e0, l0, e0};
+}
+// Value of a per-position register array at position f (f.pos >= 0).
+template <int E, typename T>
+__device__ __forceinline__ T wave_at(const T (&v)[E], WPos f) {
+    T x = v[0];
+#pragma unroll
+    for (int e = 1; e < E; e++)
+        if (e == f.e) x = v[e];
+    if constexpr (sizeof(T) == 4)
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), f.lane));
+    else
+        return x;  // (unused)
+}
+// Inclusive prefix sums over positions (f64).
+template <int E>
+__device__ __forceinline__ void wave_cum(const double (&w)[E], double (&c)[E]) {
+    double run = 0.0;
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        run += w[e];
+        c[e] = run;
+    }
+    const double pre = wave_incl_scan_d(run) - run;
+#pragma unroll
+    for (int e = 0; e < E; e++) c[e] += pre;
+}
+
+// Lists of at most 64 * E entries: wave 0 does top-k / top-p / min-p, the listing and the
+// draw or judge in registers with DPP scans and ballots, no block barrier; the other waves
+// wait for the result. E = 1: the (unsorted) keys are sorted in registers here; E > 1: the
+// keys in sm.u.cb.keys are already sorted. Returns false when the list does not decide the
+// cut (nothing has been written then).
+template <int E>
 __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const RowCtx& C, int N, bool sorted, float M,
                                              float S, ArgMax rawmax, bool exhaustive, bool minp_complete) {
     enum { R_TOK = 0, R_VERDICT = 1, R_KIND = 2 };  // R_KIND: 0 weights, 1 token target, 2 undecided
     if (wave_id() == 0) {
         const int lane = lane_id();
-        const bool valid = lane < N;
-        uint64_t key = valid ? sm.u.cb.keys[lane] : 0ull;
-        key = wave_sort_desc(key);
-        const float s = sorted ? key_s(key) : unord32((uint32_t)key);
-        const uint32_t idx = sorted ? key_idx(key) : ~(uint32_t)(key >> 32);
-        const float p = valid ? expf(s - M) / S : 0.0f;  // sample.rs:383, 388
+        bool valid[E];
+        float s[E], p[E];
+        uint32_t idx[E];
+        int64_t jj[E];
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            jj[e] = (int64_t)E * lane + e;
+            valid[e] = jj[e] < N;
+            uint64_t key = valid[e] ? sm.u.cb.keys[jj[e]] : 0ull;
+            if (E == 1) key = wave_sort_desc(key);
+            s[e] = sorted ? key_s(key) : unord32((uint32_t)key);
+            idx[e] = sorted ? key_idx(key) : ~(uint32_t)(key >> 32);
+            p[e] = valid[e] ? expf(s[e] - M) / S : 0.0f;  // sample.rs:383, 388
+        }
         const int64_t Lk = C.kmode ? C.k : a.V;
-        const int lim = (int)(Lk < N ? Lk : N);
+        const int64_t lim = Lk < N ? Lk : N;
         int64_t Lp = Lk, Lm = L_UNKNOWN;
+        double w[E], cum[E];
+        bool pred[E];
         if (sorted && C.pmode) {  // sample.rs:397-409
-            const double cum = wave_incl_scan_d((double)p);
-            const uint64_t hit = __ballot(lane < lim && cum >= (double)C.top_p);
-            if (hit) Lp = (int64_t)__ffsll((unsigned long long)hit);
+#pragma unroll
+            for (int e = 0; e < E; e++) w[e] = (double)p[e];
+            wave_cum<E>(w, cum);
+#pragma unroll
+            for (int e = 0; e < E; e++) pred[e] = jj[e] < lim && cum[e] >= (double)C.top_p;
+            const WPos f = wave_first<E>(pred);
+            if (f.pos >= 0) Lp = f.pos + 1;
             else if (!(Lk <= N || exhaustive)) Lp = L_UNKNOWN;
         }
         float thresh = 0.0f;
@@ -558,12 +678,17 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
             if (sorted) {
                 const int64_t trunc = min(Lk, Lp);
                 const int64_t n_in = trunc < N ? trunc : N;
-                const uint64_t fail = __ballot(lane < n_in && p < thresh);
-                if (fail) Lm = (int64_t)__ffsll((unsigned long long)fail) - 1;
+#pragma unroll
+                for (int e = 0; e < E; e++) pred[e] = jj[e] < n_in && p[e] < thresh;
+                const WPos f = wave_first<E>(pred);
+                if (f.pos >= 0) Lm = f.pos;
                 else if (trunc <= N) Lm = trunc;
                 else if (minp_complete || exhaustive) Lm = N;
             } else {
-                const int64_t c = __popcll(__ballot(valid && p >= thresh));
+                uint32_t c = 0;
+#pragma unroll
+                for (int e = 0; e < E; e++) c += (valid[e] && p[e] >= thresh) ? 1u : 0u;
+                c = wave_sum_u(c);
                 if (minp_complete || exhaustive) Lm = c;
             }
             if (Lm == 0) {  // sample.rs:415-422
@@ -584,48 +709,73 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
             if (!ok) kind = 2;
         }
         if (kind == 0) {
-            const int nl = sorted ? (int)(L < N ? L : N) : N;
-            const bool kept = sorted ? lane < nl : (valid && p >= thresh);
-            if (a.t_kind) {
-                const bool listed = kept && p > 0.0f;
-                const uint64_t lm = __ballot(listed);
-                const int o = __popcll(lm & lanes_below());
-                if (listed && o < a.t_cap) {
-                    a.t_ids[(int64_t)C.row * a.t_cap + o] = idx;
-                    a.t_probs[(int64_t)C.row * a.t_cap + o] = p;
+            const int64_t nl = sorted ? (L < N ? L : N) : N;
+            bool kept[E];
+#pragma unroll
+            for (int e = 0; e < E; e++) kept[e] = sorted ? jj[e] < nl : (valid[e] && p[e] >= thresh);
+            if (a.t_kind) {  // kept entries with p > 0, in draw order
+                uint32_t nlst = 0;
+#pragma unroll
+                for (int e = 0; e < E; e++) nlst += (kept[e] && p[e] > 0.0f) ? 1u : 0u;
+                const uint32_t incl = wave_scan_incl(nlst, 0u, [](uint32_t x, uint32_t y) { return x + y; });
+                uint32_t o = incl - nlst;
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    if (kept[e] && p[e] > 0.0f) {
+                        if ((int64_t)o < a.t_cap) {
+                            a.t_ids[(int64_t)C.row * a.t_cap + o] = idx[e];
+                            a.t_probs[(int64_t)C.row * a.t_cap + o] = p[e];
+                        }
+                        o++;
+                    }
                 }
+                const uint32_t total = lane63(incl);
                 if (lane == 0) {
                     a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
                     a.t_kept[C.row] = (int32_t)L;
-                    a.t_listed[C.row] = (int32_t)min((int64_t)__popcll(lm), a.t_cap);
+                    a.t_listed[C.row] = (int32_t)min((int64_t)total, a.t_cap);
                 }
             }
-            const double w = kept ? (double)p : 0.0;
-            const double cumk = wave_incl_scan_d(w);
-            const double sum = __shfl(cumk, WAVE - 1);
+#pragma unroll
+            for (int e = 0; e < E; e++) w[e] = kept[e] ? (double)p[e] : 0.0;
+            wave_cum<E>(w, cum);
+            const double sum = lane63(cum[E - 1]);
             if (!C.judged) {  // draw, sample.rs:312-323
                 const double r = (double)C.u * sum;
-                const uint64_t hit = __ballot(kept && cumk >= r);
-                const int j = hit ? __ffsll((unsigned long long)hit) - 1 : 0;
-                tok = __shfl(idx, j);
+#pragma unroll
+                for (int e = 0; e < E; e++) pred[e] = kept[e] && cum[e] >= r;
+                WPos f = wave_first<E>(pred);
+                if (f.pos < 0) f = WPos{0, 0, 0};
+                tok = wave_at<E>(idx, f);
             } else {  // judge, spec.rs:83-95
-                const uint64_t dm = __ballot(kept && idx == C.draft);
-                const int pd = dm ? __ffsll((unsigned long long)dm) - 1 : -1;
-                const double p_d = pd >= 0 ? (double)__shfl(p, pd) : 0.0;
+#pragma unroll
+                for (int e = 0; e < E; e++) pred[e] = kept[e] && idx[e] == C.draft;
+                const WPos fd = wave_first<E>(pred);
+                const double p_d = fd.pos >= 0 ? (double)wave_at<E>(p, fd) : 0.0;
                 if (sum > 0.0 && (double)C.u < p_d / sum) {
                     tok = C.draft;
                     verdict = 1;
                 } else {
-                    const bool res = kept && lane != pd;
-                    if (__ballot(res && p > 0.0f) == 0) {  // residual empty or all <= 0
+                    bool res[E];
+                    bool anypos = false;
+#pragma unroll
+                    for (int e = 0; e < E; e++) {
+                        res[e] = kept[e] && jj[e] != fd.pos;
+                        anypos = anypos || (res[e] && p[e] > 0.0f);
+                    }
+                    if (__ballot(anypos) == 0) {  // residual empty or all <= 0
                         tok = C.draft;
                         verdict = 1;
                     } else {
-                        const double cum2 = wave_incl_scan_d(res ? (double)p : 0.0);
+#pragma unroll
+                        for (int e = 0; e < E; e++) w[e] = res[e] ? (double)p[e] : 0.0;
+                        wave_cum<E>(w, cum);
                         const double r2 = (double)C.u2 * (sum - p_d);
-                        const uint64_t hit = __ballot(res && cum2 >= r2);
-                        const int j = hit ? __ffsll((unsigned long long)hit) - 1 : 0;
-                        tok = __shfl(idx, j);
+#pragma unroll
+                        for (int e = 0; e < E; e++) pred[e] = res[e] && cum[e] >= r2;
+                        WPos f = wave_first<E>(pred);
+                        if (f.pos < 0) f = WPos{0, 0, 0};
+                        tok = wave_at<E>(idx, f);
                         verdict = 0;
                     }
                 }
@@ -671,11 +821,7 @@ __device__ __forceinline__ int combine_list(const KArgs& a, Smem& sm, const RowC
                                             float S, ArgMax rawmax, bool exhaustive, bool minp_complete,
                                             int64_t tb) {
     const int tid = threadIdx.x;
-    int n2 = 64;
-    while (n2 < N) n2 <<= 1;
-    for (int j = N + tid; j < n2; j += BLOCK) sm.u.cb.keys[j] = 0ull;
-    __syncthreads();
-    bitonic_sort_desc(sm.u.cb.keys, n2);
+    sort_list(sm, N);
     BFI_TRACE(a, tb, 5);
     // probabilities of the sorted positions: p = expf(s - M) / S (sample.rs:383, 388)
     for (int j = tid; j < N; j += BLOCK) {
@@ -920,7 +1066,12 @@ __device__ __forceinline__ int combine_bounded(const KArgs& a, Smem& sm, const R
         const bool exhaustive = !(th > -__builtin_inff());
         const bool minp_complete = th <= th_m;
         if (N <= WAVE) {
-            if (combine_wave(a, sm, C, N, sorted, M, S, rawmax, exhaustive, minp_complete)) return CB_DONE;
+            if (combine_wave<1>(a, sm, C, N, sorted, M, S, rawmax, exhaustive, minp_complete)) return CB_DONE;
+        } else if (N <= 8 * WAVE) {
+            if (N <= BLOCK) sort_list_regs(sm, N);
+            else sort_list(sm, N);
+            BFI_TRACE(a, tb, 5);
+            if (combine_wave<8>(a, sm, C, N, sorted, M, S, rawmax, exhaustive, minp_complete)) return CB_DONE;
         } else {
             const int r = combine_list(a, sm, C, N, sorted, M, S, rawmax, exhaustive, minp_complete, tb);
             if (r >= 0) return r;
