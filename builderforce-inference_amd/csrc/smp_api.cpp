@@ -359,8 +359,7 @@ int64_t bfi_smp_trace(bfi_smp_ctx* ctx, uint64_t* out, int64_t max_words) {
 
 int bfi_smp_set_profiling(bfi_smp_ctx* ctx, int enabled) {
     if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
-    ctx->profiling = enabled != 0;
-    ctx->ev_used = 0;
+    ctx->profiling = enabled != 0;  // the record persists until bfi_smp_profile reads it
     return BFI_SMP_OK;
 }
 

@@ -159,9 +159,21 @@ __device__ __forceinline__ int hist_find(const Smem& sm, uint32_t id) {
 // `after_clear()` runs between the two barriers (LDS written there is visible on return).
 // Returns false when the row has more than HMAX distinct ids (inserts stop there, so the
 // table never fills and every probe sequence ends).
+constexpr int HB = 4;  // history entries per thread per round
+
+// The ids this thread inserted first (single-round histories): their slots and masked
+// logits stay in registers, so the logit loads can land while the table is finished.
+struct HistOwn {
+    bool regs;         // the owner lists below are complete (else hraw holds the logits)
+    uint32_t own;      // bit g: entry g was inserted by this thread
+    uint32_t id[HB];
+    uint32_t slot[HB];
+    uint32_t mw[HB];   // allow-mask word of the id
+    float x[HB];       // logit
+};
+
 template <bool BF16, typename F>
-__device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCtx& C, F after_clear) {
-    constexpr int HB = 4;
+__device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCtx& C, HistOwn& ho, F after_clear) {
     const int tid = threadIdx.x;
     for (int k = tid; k < HSLOTS; k += BLOCK) {
         sm.hkey[k] = HEMPTY;
@@ -170,22 +182,23 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
     if (tid == 0) sm.misc[MISC_HN] = 0;
     const int64_t H = C.pen_on ? C.h.size() : 0;
     const uint32_t V = (uint32_t)a.V;
+    ho.regs = H <= (int64_t)HB * BLOCK;
+    ho.own = 0;
     bool cleared = false;
     for (int64_t j0 = 0; j0 < H; j0 += (int64_t)HB * BLOCK) {
-        uint32_t id[HB], mw[HB];
-        float x[HB];
+        uint32_t* mw = ho.mw;
 #pragma unroll
         for (int g = 0; g < HB; g++) {
             const int64_t j = j0 + g * BLOCK + tid;
-            id[g] = j < H ? C.h.at(j) : HEMPTY;
+            ho.id[g] = j < H ? C.h.at(j) : HEMPTY;
         }
 #pragma unroll
         for (int g = 0; g < HB; g++) {
-            const uint32_t ld = id[g] < V ? id[g] : 0u;
+            const uint32_t ld = ho.id[g] < V ? ho.id[g] : 0u;
             if (BF16)
-                x[g] = __uint_as_float((uint32_t)((const uint16_t*)a.logits)[(int64_t)C.row * a.row_stride + ld] << 16);
+                ho.x[g] = __uint_as_float((uint32_t)((const uint16_t*)a.logits)[(int64_t)C.row * a.row_stride + ld] << 16);
             else
-                x[g] = ((const float*)a.logits)[(int64_t)C.row * a.row_stride + ld];
+                ho.x[g] = ((const float*)a.logits)[(int64_t)C.row * a.row_stride + ld];
             mw[g] = C.mrow ? C.mrow[ld >> 5] : 0xFFFFFFFFu;
         }
         if (!cleared) {
@@ -195,18 +208,21 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
         }
 #pragma unroll
         for (int g = 0; g < HB; g++) {
-            if (id[g] >= V) continue;
+            const uint32_t id = ho.id[g];
+            if (id >= V) continue;
             if (__hip_atomic_load((BFI_LDS uint32_t*)&sm.misc[MISC_HN], __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_WORKGROUP) > (uint32_t)HMAX)
                 continue;
-            uint32_t k = hslot0(id[g]);
+            uint32_t k = hslot0(id);
             for (int probe = 0; probe < HSLOTS; probe++) {
-                const uint32_t prev = lds_cas(&sm.hkey[k], HEMPTY, id[g]);
-                if (prev == HEMPTY || prev == id[g]) {
+                const uint32_t prev = lds_cas(&sm.hkey[k], HEMPTY, id);
+                if (prev == HEMPTY || prev == id) {
                     if (prev == HEMPTY) {
                         const uint32_t pos = lds_add(&sm.misc[MISC_HN], 1u);  // < HSLOTS: one per key
                         sm.hlist[pos] = (uint16_t)k;
-                        sm.hraw[k] = ((mw[g] >> (id[g] & 31)) & 1u) ? x[g] : -__builtin_inff();
+                        ho.own |= 1u << g;
+                        ho.slot[g] = k;
+                        if (!ho.regs) sm.hraw[k] = ((mw[g] >> (id & 31)) & 1u) ? ho.x[g] : -__builtin_inff();
                     }
                     lds_add(&sm.hcnt[k], 1u);
                     break;
@@ -256,14 +272,10 @@ __device__ __forceinline__ float unord_or_ninf(uint32_t o) { return o ? unord32(
 // expression), in 2^52 fixed point. A history id equal to its chunk's maximum marks the
 // chunk dirty (cflag, ag.nd). Row aggregates: the largest hpen (ag.hmax), or for greedy
 // rows the argmax key (ag.gkey). sm.cm / sm.cxm must hold the chunk results.
-__device__ __forceinline__ void hist_values(const KArgs& a, Smem& sm, const RowCtx& C) {
-    const int nh = (int)sm.misc[MISC_HN];
+__device__ __forceinline__ void hist_values(const KArgs& a, Smem& sm, const RowCtx& C, const HistOwn& ho) {
     uint64_t gk = 0;
     uint32_t hm = 0, nd = 0;
-    for (int j = threadIdx.x; j < nh; j += BLOCK) {
-        const int k = sm.hlist[j];
-        const uint32_t id = sm.hkey[k];
-        const float x = sm.hraw[k];  // masked logit
+    auto one = [&](uint32_t k, uint32_t id, float x) __attribute__((always_inline)) {  // x: masked logit
         const float vr = raw_value(C, x, true), vp = pen_value(C, x, true, sm.hcnt[k]);
         sm.hraw[k] = vr;
         sm.hpen[k] = vp;
@@ -282,6 +294,18 @@ __device__ __forceinline__ void hist_values(const KArgs& a, Smem& sm, const RowC
                 nd++;
             }
         }
+    };
+    if (ho.regs) {
+#pragma unroll
+        for (int g = 0; g < HB; g++)
+            if ((ho.own >> g) & 1u)
+                one(ho.slot[g], ho.id[g], ((ho.mw[g] >> (ho.id[g] & 31)) & 1u) ? ho.x[g] : -__builtin_inff());
+    } else {
+        const int nh = (int)sm.misc[MISC_HN];
+        for (int j = threadIdx.x; j < nh; j += BLOCK) {
+            const int k = sm.hlist[j];
+            one((uint32_t)k, sm.hkey[k], sm.hraw[k]);
+        }
     }
     if (C.greedy)
         wave_lds_max64(&sm.ag.gkey, gk);
@@ -298,7 +322,7 @@ __device__ __forceinline__ uint32_t wave_append(uint32_t* ctr, bool pred) {
     const int leader = __ffsll((unsigned long long)m) - 1;
     uint32_t base = 0;
     if (lane_id() == leader) base = lds_add(ctr, (uint32_t)__popcll(m));
-    base = __shfl(base, leader);
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
     return base + (uint32_t)__popcll(m & lanes_below());
 }
 
@@ -997,13 +1021,32 @@ __device__ __forceinline__ CandBatch load_cands(const KArgs& a, const Smem& sm, 
 // Appends the non-history candidates of B whose exact value is >= th to the list. Every
 // thread of the block calls it (wave_append).
 __device__ __forceinline__ void append_cands(Smem& sm, const RowCtx& C, const CandBatch& B, float th, bool sorted) {
+    float v[GU];
+    uint32_t take = 0;  // bit g: entry g is appended
 #pragma unroll
     for (int g = 0; g < GU; g++) {
-        const float v = raw_value(C, B.cd[g].x, true);  // masked logit / T, exact
-        const bool take = v >= th && v > -__builtin_inff() && !(C.pen_on && hist_find(sm, B.cd[g].idx) >= 0);
-        const uint32_t slot = wave_append(&sm.misc[MISC_N], take);
-        if (take && slot < NMAX)
-            sm.u.cb.keys[slot] = sorted ? key64(v, B.cd[g].idx) : (((uint64_t)(~B.cd[g].idx) << 32) | ord32(v));
+        v[g] = raw_value(C, B.cd[g].x, true);  // masked logit / T, exact
+        if (v[g] >= th && v[g] > -__builtin_inff() && !(C.pen_on && hist_find(sm, B.cd[g].idx) >= 0))
+            take |= 1u << g;
+    }
+    // one reservation per wave for all its entries
+    const uint32_t n = (uint32_t)__popc(take);
+    const uint32_t incl = wave_scan_incl(n, 0u, [](uint32_t x, uint32_t y) { return x + y; });
+    const uint32_t tot = lane63(incl);
+    uint32_t base = 0;
+    if (tot) {
+        if (lane_id() == 0) base = lds_add(&sm.misc[MISC_N], tot);
+        base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    }
+    uint32_t slot = base + incl - n;
+#pragma unroll
+    for (int g = 0; g < GU; g++) {
+        if ((take >> g) & 1u) {
+            if (slot < NMAX)
+                sm.u.cb.keys[slot] = sorted ? key64(v[g], B.cd[g].idx)
+                                            : (((uint64_t)(~B.cd[g].idx) << 32) | ord32(v[g]));
+            slot++;
+        }
     }
 }
 
@@ -1761,7 +1804,8 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
         sm.ag.flags = 0u;
         sm.ag.nd = 0u;
     }
-    const bool hashed = hist_build<BF16>(a, sm, C, [&]() {
+    HistOwn ho;
+    const bool hashed = hist_build<BF16>(a, sm, C, ho, [&]() {
         if (tid < nc) {
             sm.cm[tid] = mine.m;
             sm.cxm[tid] = mine.raw_m;
@@ -1806,7 +1850,7 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
         // ---- B: history values (sample.rs:331-375) and the streaming terms they replace
         uint32_t dirty = 0;
         if (C.pen_on) {
-            hist_values(a, sm, C);
+            hist_values(a, sm, C, ho);
             if (sm.ag.nd) {
                 // rare: a chunk whose maximum is a history id; re-read it for the max and
                 // sum of its other elements, then refresh the aggregates

@@ -82,8 +82,9 @@ int bfi_smp_abi_version(void);
 /* Profiling (no counterpart in the reference; for benchmarks): while enabled, every launch
  * times its two kernels (the streaming pass over the logits, then the per-row selection)
  * with start/stop HIP events recorded in the kernels' own dispatch packets on the caller's
- * stream, so launch gaps are excluded. bfi_smp_profile waits for the recorded launches,
- * returns the summed kernel times in ms and clears the record (at most 65536 launches). */
+ * stream, so launch gaps are excluded. Profiling may be switched on for some launches only;
+ * the record keeps them until bfi_smp_profile waits for them, returns the summed kernel
+ * times in ms and clears it (at most 65536 launches). */
 int bfi_smp_set_profiling(bfi_smp_ctx *ctx, int enabled);
 int bfi_smp_profile(bfi_smp_ctx *ctx, double *stream_ms, double *select_ms, int64_t *launches);
 
