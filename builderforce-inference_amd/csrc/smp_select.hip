@@ -1071,6 +1071,59 @@ __device__ __forceinline__ uint32_t chunk_take(const ChunkPart& mine, float th) 
     return (mine.theta <= th && mine.m >= th) ? mine.ncand : 0u;
 }
 
+// Top-k rows whose list above th holds more than NMAX entries: a bound t >= th with at least
+// k entries at or above it (and, buckets being narrow, usually few more), from a histogram
+// of the entries' values in 1/32-wide buckets below M (2048 buckets). The entries are the
+// current candidate ranges (sm.cpre) and the history ids. Returns th when the k-th largest
+// lies in the last bucket.
+__device__ __forceinline__ float topk_bound(const KArgs& a, Smem& sm, const RowCtx& C, float M, float th) {
+    constexpr int NBK = 2048;
+    constexpr float R = 32.0f;
+    constexpr int BPT = NBK / BLOCK;
+    const int tid = threadIdx.x;
+    const int nc = a.n_chunks;
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(sm.u.cb.keys);  // the list is rebuilt afterwards
+    for (int b = tid; b < NBK; b += BLOCK) cnt[b] = 0u;
+    __syncthreads();
+    auto bucket = [&](float v) -> uint32_t {
+        const float d = (M - v) * R;
+        return d < (float)(NBK - 1) ? (uint32_t)d : (uint32_t)(NBK - 1);
+    };
+    for (uint32_t b0 = 0; b0 < sm.cpre[nc]; b0 += GU * BLOCK) {  // uniform trip count
+        const CandBatch B = load_cands(a, sm, C.row, nc, b0);
+#pragma unroll
+        for (int g = 0; g < GU; g++) {
+            const float v = raw_value(C, B.cd[g].x, true);
+            if (v >= th && v > -__builtin_inff() && !(C.pen_on && hist_find(sm, B.cd[g].idx) >= 0))
+                lds_add(&cnt[bucket(v)], 1u);
+        }
+    }
+    if (C.pen_on) {
+        for (int j = tid; j < (int)sm.misc[MISC_HN]; j += BLOCK) {
+            const float v = sm.hpen[sm.hlist[j]];
+            if (v >= th && v > -__builtin_inff()) lds_add(&cnt[bucket(v)], 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t loc[BPT], run = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; i++) {
+        run += cnt[tid * BPT + i];
+        loc[i] = run;
+    }
+    uint32_t tot;
+    const uint32_t pre = block_excl_scan<uint32_t>(run, sm.ru, tot);
+    uint32_t hit = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < BPT; i++)
+        if (hit == 0xFFFFFFFFu && pre + loc[i] >= (uint32_t)C.k) hit = (uint32_t)(tid * BPT + i);
+    hit = block_min_u(hit, sm.ru);
+    if (hit >= (uint32_t)(NBK - 1)) return th;
+    // every entry of buckets 0..hit is >= this (the margins cover the rounding of the index)
+    const float t = M - ((float)(hit + 1) / R) * (1.0f + 1e-6f) - 1e-6f * (fabsf(M) + 1.0f);
+    return fmaxf(th, t);
+}
+
 // `th_raw`: every non-history element >= th_raw is some chunk's candidate (the largest chunk
 // bound). `list_ready`: the first pass's list (complete above max(th_raw, min-p bound)) is
 // already in sm.u.cb.keys with its length in MISC_N.
@@ -1102,7 +1155,18 @@ __device__ __forceinline__ int combine_bounded(const KArgs& a, Smem& sm, const R
                 __syncthreads();
             }
         }
-        const int N = (int)sm.misc[MISC_N];
+        int N = (int)sm.misc[MISC_N];
+        if (N > NMAX && pass == 0 && C.kmode && C.k <= NMAX / 2) {
+            // top-k needs only the k largest: raise th to a bound holding about k entries
+            th = topk_bound(a, sm, C, M, th);
+            if (tid == 0) sm.misc[MISC_N] = 0;
+            __syncthreads();
+            for (uint32_t b0 = 0; b0 < sm.cpre[nc]; b0 += GU * BLOCK)  // uniform trip count
+                append_cands(sm, C, load_cands(a, sm, C.row, nc, b0), th, sorted);
+            append_hist(sm, C, th, sorted);
+            __syncthreads();
+            N = (int)sm.misc[MISC_N];
+        }
         BFI_TRACE(a, tb, 4);
         if (a.trace && tid == 0) sm.tr[6] = ((uint64_t)sm.cpre[nc] << 32) | (uint32_t)N;
         if (N > NMAX) return CB_RADIX;

@@ -383,3 +383,21 @@ def test_extreme_magnitudes(smp):
     cfg = _cfg_from(rows, params, u=[0.3, 0.6, 0.9, 0.1])
     cfg["name"] = "magnitudes"
     check(cfg, 256, smp)
+
+
+def test_c1_full_size_and_topk_over_many_chunks(smp):
+    """B=1 at full vocabulary: 75 chunks each hand over their own top-k, so the list above
+    the largest chunk bound holds thousands of entries and the select narrows it to about k."""
+    cfg = workloads.config("C1", seed=0)
+    check(cfg, 2048, smp)
+    rng = np.random.default_rng(15)
+    V = 151936
+    rows = [(rng.standard_normal(V) * 2.5).astype(np.float32) for _ in range(4)]
+    params = [dict(temperature=0.7, top_k=40, top_p=0.95), dict(temperature=1.2, top_k=200),
+              dict(temperature=1.0, top_k=1000, top_p=0.99), dict(temperature=0.9, top_k=40, min_p=0.01)]
+    hist = [rng.integers(0, V, 64).tolist(), [], rng.integers(0, V, 300).tolist(), []]
+    for i in range(4):
+        params[i]["repeat_penalty"] = 1.1 if hist[i] else 1.0
+        cfg = _cfg_from([rows[i]], [params[i]], [hist[i]], u=[0.3 + 0.2 * i])
+        cfg["name"] = f"topk-many-chunks-{i}"
+        check(cfg, 2048, smp)
