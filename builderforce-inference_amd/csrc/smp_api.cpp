@@ -121,7 +121,7 @@ Layout layout(int64_t n_rows, const Shape& s, int bm_words) {
     L.row_pen = off;
     off = align_up(off + (size_t)n_rows * (2 * (size_t)bm_words + bfi::GDCAP) * sizeof(uint32_t), 256);
     L.row_hist = off;
-    off = align_up(off + (size_t)n_rows * bfi::NBUCKET * 2 * sizeof(uint64_t), 256);
+    off = align_up(off + (size_t)n_rows * bfi::NVB * 2 * sizeof(uint64_t), 256);
     L.total = off;
     return L;
 }

@@ -24,7 +24,8 @@ constexpr int CHUNK_MAX = 8192;        // logits elements per workgroup (stream 
 constexpr int NCMAX = 256;             // chunks per row
 constexpr int CAND_CAP = 2048;         // candidates one chunk may hand to the combine
 constexpr int NMAX = 2048;             // combine sort capacity (power of two)
-constexpr int NBUCKET = 1024;          // radix buckets (10-bit digits) of the fallback select
+constexpr int NBUCKET = 1024;          // radix buckets (10-bit key digits) of the fallback select
+constexpr int NVB = 2048;              // value buckets of the row select (1/32 wide below the row max)
 constexpr int DCAP = 1024;             // distinct history ids counted per chunk in LDS
 constexpr int GDCAP = 4096;            // distinct history ids counted per row (global scratch)
 constexpr int HSLOTS_LOG2 = 11;
@@ -95,7 +96,7 @@ struct KArgs {
     uint32_t* seq_ctr;
     uint32_t* row_res;   // verify: 2 words per row {verdict, token}
     uint32_t* row_pen;   // fallback select: per row bm[bm_words] + pre[bm_words] + cnt[GDCAP]
-    uint64_t* row_hist;  // fallback select: per row level-1 histogram (count, mass) x NBUCKET
+    uint64_t* row_hist;  // row select: per row value histogram (mass, count) x NVB
     int32_t bm_words;
     uint64_t* trace;  // optional phase timestamps (wall clock) per workgroup
 };

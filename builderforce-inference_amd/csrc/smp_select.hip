@@ -39,8 +39,8 @@ struct __align__(16) Smem {
             float p[NMAX];
         } cb;
         struct {
-            uint64_t mass[NBUCKET];
-            uint32_t cnt[NBUCKET];
+            uint64_t mass[NVB];
+            uint32_t cnt[NVB];
         } hs;
     } u;
     // history set of the row (ids < V): open addressing, linear probing
@@ -186,7 +186,6 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
     ho.own = 0;
     bool cleared = false;
     for (int64_t j0 = 0; j0 < H; j0 += (int64_t)HB * BLOCK) {
-        uint32_t* mw = ho.mw;
 #pragma unroll
         for (int g = 0; g < HB; g++) {
             const int64_t j = j0 + g * BLOCK + tid;
@@ -199,7 +198,7 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
                 ho.x[g] = __uint_as_float((uint32_t)((const uint16_t*)a.logits)[(int64_t)C.row * a.row_stride + ld] << 16);
             else
                 ho.x[g] = ((const float*)a.logits)[(int64_t)C.row * a.row_stride + ld];
-            mw[g] = C.mrow ? C.mrow[ld >> 5] : 0xFFFFFFFFu;
+            ho.mw[g] = C.mrow ? C.mrow[ld >> 5] : 0xFFFFFFFFu;
         }
         if (!cleared) {
             __syncthreads();
@@ -222,7 +221,7 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
                         sm.hlist[pos] = (uint16_t)k;
                         ho.own |= 1u << g;
                         ho.slot[g] = k;
-                        if (!ho.regs) sm.hraw[k] = ((mw[g] >> (id & 31)) & 1u) ? ho.x[g] : -__builtin_inff();
+                        if (!ho.regs) sm.hraw[k] = ((ho.mw[g] >> (id & 31)) & 1u) ? ho.x[g] : -__builtin_inff();
                     }
                     lds_add(&sm.hcnt[k], 1u);
                     break;
@@ -388,10 +387,12 @@ __device__ __forceinline__ void span_pass(const KArgs& a, const Smem& sm, const 
     constexpr int EPV = Elem<BF16>::EPV;
     constexpr uint32_t TILE = (uint32_t)BLOCK * VEC * EPV;
     const uint32_t em = (1u << EPV) - 1u;
+    // the next tile's loads are issued before this tile is processed
+    float x[VEC][EPV], xn[VEC][EPV];
+    if (c0 < c1) load_tile<BF16, VEC>(a, C.row, c0, min(c0 + TILE, c1), x);
     for (uint32_t t0 = c0; t0 < c1; t0 += TILE) {
         const uint32_t t1 = min(t0 + TILE, c1);
-        float x[VEC][EPV];
-        load_tile<BF16, VEC>(a, C.row, t0, t1, x);
+        if (t1 < c1) load_tile<BF16, VEC>(a, C.row, t1, min(t1 + TILE, c1), xn);
         if (!SKIP_HIST) transform_tile<BF16, VEC>(sm, C, P, t0, t1, x);
 #pragma unroll
         for (int q = 0; q < VEC; q++) {
@@ -411,6 +412,10 @@ __device__ __forceinline__ void span_pass(const KArgs& a, const Smem& sm, const 
                 }
             }
         }
+#pragma unroll
+        for (int q = 0; q < VEC; q++)
+#pragma unroll
+            for (int e = 0; e < EPV; e++) x[q][e] = xn[q][e];
     }
 }
 
@@ -620,7 +625,7 @@ struct WPos {
 template <int E>
 __device__ __forceinline__ WPos wave_first(const bool (&pred)[E]) {
     int fe = E;
-#pragma unroll
+#pragma clang loop unroll(full)
     for (int e = E - 1; e >= 0; e--)
         if (pred[e]) fe = e;
     const uint64_t hit = __ballot(fe < E);
@@ -632,26 +637,28 @@ __device__ __forceinline__ WPos wave_first(const bool (&pred)[E]) {
 // Value of a per-position register array at position f (f.pos >= 0).
 template <int E, typename T>
 __device__ __forceinline__ T wave_at(const T (&v)[E], WPos f) {
-    T x = v[0];
-#pragma unroll
-    for (int e = 1; e < E; e++)
-        if (e == f.e) x = v[e];
-    if constexpr (sizeof(T) == 4)
-        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), f.lane));
-    else
-        return x;  // (unused)
+    static_assert(sizeof(T) == 4, "32-bit values");
+    // read every candidate from lane f.lane (wave-uniform values), then pick f.e: no
+    // dynamically indexed register array
+    uint32_t x = 0;
+#pragma clang loop unroll(full)
+    for (int e = 0; e < E; e++) {
+        const uint32_t r = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, v[e]), f.lane);
+        x = e == f.e ? r : x;
+    }
+    return __builtin_bit_cast(T, x);
 }
 // Inclusive prefix sums over positions (f64).
 template <int E>
 __device__ __forceinline__ void wave_cum(const double (&w)[E], double (&c)[E]) {
     double run = 0.0;
-#pragma unroll
+#pragma clang loop unroll(full)
     for (int e = 0; e < E; e++) {
         run += w[e];
         c[e] = run;
     }
     const double pre = wave_incl_scan_d(run) - run;
-#pragma unroll
+#pragma clang loop unroll(full)
     for (int e = 0; e < E; e++) c[e] += pre;
 }
 
@@ -670,7 +677,7 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
         float s[E], p[E];
         uint32_t idx[E];
         int64_t jj[E];
-#pragma unroll
+#pragma clang loop unroll(full)
         for (int e = 0; e < E; e++) {
             jj[e] = (int64_t)E * lane + e;
             valid[e] = jj[e] < N;
@@ -686,10 +693,10 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
         double w[E], cum[E];
         bool pred[E];
         if (sorted && C.pmode) {  // sample.rs:397-409
-#pragma unroll
+#pragma clang loop unroll(full)
             for (int e = 0; e < E; e++) w[e] = (double)p[e];
             wave_cum<E>(w, cum);
-#pragma unroll
+#pragma clang loop unroll(full)
             for (int e = 0; e < E; e++) pred[e] = jj[e] < lim && cum[e] >= (double)C.top_p;
             const WPos f = wave_first<E>(pred);
             if (f.pos >= 0) Lp = f.pos + 1;
@@ -702,7 +709,7 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
             if (sorted) {
                 const int64_t trunc = min(Lk, Lp);
                 const int64_t n_in = trunc < N ? trunc : N;
-#pragma unroll
+#pragma clang loop unroll(full)
                 for (int e = 0; e < E; e++) pred[e] = jj[e] < n_in && p[e] < thresh;
                 const WPos f = wave_first<E>(pred);
                 if (f.pos >= 0) Lm = f.pos;
@@ -710,7 +717,7 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
                 else if (minp_complete || exhaustive) Lm = N;
             } else {
                 uint32_t c = 0;
-#pragma unroll
+#pragma clang loop unroll(full)
                 for (int e = 0; e < E; e++) c += (valid[e] && p[e] >= thresh) ? 1u : 0u;
                 c = wave_sum_u(c);
                 if (minp_complete || exhaustive) Lm = c;
@@ -735,15 +742,15 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
         if (kind == 0) {
             const int64_t nl = sorted ? (L < N ? L : N) : N;
             bool kept[E];
-#pragma unroll
+#pragma clang loop unroll(full)
             for (int e = 0; e < E; e++) kept[e] = sorted ? jj[e] < nl : (valid[e] && p[e] >= thresh);
             if (a.t_kind) {  // kept entries with p > 0, in draw order
                 uint32_t nlst = 0;
-#pragma unroll
+#pragma clang loop unroll(full)
                 for (int e = 0; e < E; e++) nlst += (kept[e] && p[e] > 0.0f) ? 1u : 0u;
                 const uint32_t incl = wave_scan_incl(nlst, 0u, [](uint32_t x, uint32_t y) { return x + y; });
                 uint32_t o = incl - nlst;
-#pragma unroll
+#pragma clang loop unroll(full)
                 for (int e = 0; e < E; e++) {
                     if (kept[e] && p[e] > 0.0f) {
                         if ((int64_t)o < a.t_cap) {
@@ -760,19 +767,19 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
                     a.t_listed[C.row] = (int32_t)min((int64_t)total, a.t_cap);
                 }
             }
-#pragma unroll
+#pragma clang loop unroll(full)
             for (int e = 0; e < E; e++) w[e] = kept[e] ? (double)p[e] : 0.0;
             wave_cum<E>(w, cum);
             const double sum = lane63(cum[E - 1]);
             if (!C.judged) {  // draw, sample.rs:312-323
                 const double r = (double)C.u * sum;
-#pragma unroll
+#pragma clang loop unroll(full)
                 for (int e = 0; e < E; e++) pred[e] = kept[e] && cum[e] >= r;
                 WPos f = wave_first<E>(pred);
                 if (f.pos < 0) f = WPos{0, 0, 0};
                 tok = wave_at<E>(idx, f);
             } else {  // judge, spec.rs:83-95
-#pragma unroll
+#pragma clang loop unroll(full)
                 for (int e = 0; e < E; e++) pred[e] = kept[e] && idx[e] == C.draft;
                 const WPos fd = wave_first<E>(pred);
                 const double p_d = fd.pos >= 0 ? (double)wave_at<E>(p, fd) : 0.0;
@@ -782,7 +789,7 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
                 } else {
                     bool res[E];
                     bool anypos = false;
-#pragma unroll
+#pragma clang loop unroll(full)
                     for (int e = 0; e < E; e++) {
                         res[e] = kept[e] && jj[e] != fd.pos;
                         anypos = anypos || (res[e] && p[e] > 0.0f);
@@ -791,11 +798,11 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
                         tok = C.draft;
                         verdict = 1;
                     } else {
-#pragma unroll
+#pragma clang loop unroll(full)
                         for (int e = 0; e < E; e++) w[e] = res[e] ? (double)p[e] : 0.0;
                         wave_cum<E>(w, cum);
                         const double r2 = (double)C.u2 * (sum - p_d);
-#pragma unroll
+#pragma clang loop unroll(full)
                         for (int e = 0; e < E; e++) pred[e] = res[e] && cum[e] >= r2;
                         WPos f = wave_first<E>(pred);
                         if (f.pos < 0) f = WPos{0, 0, 0};
@@ -1419,7 +1426,9 @@ __device__ __forceinline__ void row_pass(const KArgs& a, Smem& sm, const RowCtx&
 
 // Finds the element at a sorted position (kind 0: 0-based position `target`) or the first
 // element whose inclusive fixed-point cumulative mass reaches `target` (kind 1), over the
-// order of key64 descending, skipping the element with key `excl`.
+// order of key64 descending, skipping the element with key `excl`: 10-bit key digits from
+// the top, one row pass per digit. The general fallback of vsel_query (targets among -inf
+// elements, value buckets too dense to sort in LDS).
 template <bool BF16, int VEC>
 __device__ __forceinline__ Sel radix_select(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, float M,
                             double scale, int kind, uint64_t target, uint64_t excl, uint64_t excl_mass) {
@@ -1427,24 +1436,12 @@ __device__ __forceinline__ Sel radix_select(const KArgs& a, Smem& sm, const RowC
     uint64_t prefix = 0;
     int pbits = 0;
     uint64_t before_cnt = 0, before_mass = 0;
-    uint64_t* saved = a.row_hist + (int64_t)C.row * NBUCKET * 2;
+    (void)excl_mass;
     for (int level = 0;; level++) {
         const int w = (64 - pbits) >= 10 ? 10 : 64 - pbits;
         const int shift = 64 - pbits - w;
         const uint32_t nb = 1u << w;
-        if (level == 0) {  // the level-1 histogram saved by radix_l1 (minus `excl`)
-            for (uint32_t b = tid; b < NBUCKET; b += BLOCK) {
-                sm.u.hs.mass[b] = saved[2 * b];
-                sm.u.hs.cnt[b] = (uint32_t)saved[2 * b + 1];
-            }
-            __syncthreads();
-            if (excl != ~0ull && tid == 0) {
-                uint32_t b = (uint32_t)(excl >> 54);
-                sm.u.hs.cnt[b] -= 1;
-                sm.u.hs.mass[b] -= excl_mass;
-            }
-            __syncthreads();
-        } else {
+        {
             for (uint32_t b = tid; b < NBUCKET; b += BLOCK) {
                 sm.u.hs.mass[b] = 0;
                 sm.u.hs.cnt[b] = 0;
@@ -1577,35 +1574,168 @@ __device__ __forceinline__ Sel radix_select(const KArgs& a, Smem& sm, const RowC
     }
 }
 
-// Level-1 histogram (top 10 key bits) of the whole row, saved to global scratch for every
-// later query of this row; returns the total fixed-point mass.
+// ---- row select by value buckets ------------------------------------------------------
+//
+// Bucket b holds the elements with (M - s) * 32 in [b, b + 1); the last bucket also takes
+// everything further below M. -inf elements (mass 0, last in the order) are in none. A
+// query finds its bucket from the bucket prefix, then gathers that bucket in one row pass,
+// sorts it in LDS and walks it.
+
+__device__ __forceinline__ uint32_t vbucket(float s, float M) {
+    const float d = (M - s) * 32.0f;
+    return d < (float)(NVB - 1) ? (uint32_t)d : (uint32_t)(NVB - 1);
+}
+
+// The row's value histogram (count, fixed-point mass), saved to global scratch for every
+// query of this row; returns the total fixed-point mass. *n_finite receives the count.
 template <bool BF16, int VEC>
-__device__ __forceinline__ uint64_t radix_l1(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, float M, double scale) {
+__device__ __forceinline__ uint64_t vsel_l1(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, float M,
+                                            double scale, uint64_t* n_finite) {
     const int tid = threadIdx.x;
-    for (uint32_t b = tid; b < NBUCKET; b += BLOCK) {
+    for (uint32_t b = tid; b < NVB; b += BLOCK) {
         sm.u.hs.mass[b] = 0;
         sm.u.hs.cnt[b] = 0;
     }
     __syncthreads();
-    row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) __attribute__((always_inline)) {
-        uint32_t b = (uint32_t)(key64(s, id) >> 54);
+    row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t, float s) __attribute__((always_inline)) {
+        if (!(s > -__builtin_inff())) return;
+        const uint32_t b = vbucket(s, M);
         lds_add(&sm.u.hs.cnt[b], 1u);
-        uint64_t m = efix_of(s, M, scale);
+        const uint64_t m = efix_of(s, M, scale);
         if (m) lds_add64(&sm.u.hs.mass[b], m);
     });
     __syncthreads();
-    uint64_t* saved = a.row_hist + (int64_t)C.row * NBUCKET * 2;
-    uint64_t m = 0;
-    for (uint32_t b = tid; b < NBUCKET; b += BLOCK) {
+    uint64_t* saved = a.row_hist + (int64_t)C.row * NVB * 2;
+    uint64_t m = 0, c = 0;
+    for (uint32_t b = tid; b < NVB; b += BLOCK) {
         saved[2 * b] = sm.u.hs.mass[b];
         saved[2 * b + 1] = sm.u.hs.cnt[b];
         m += sm.u.hs.mass[b];
+        c += sm.u.hs.cnt[b];
     }
-    uint64_t tot;
+    uint64_t tot, ctot;
     block_excl_scan<uint64_t>(m, sm.r64, tot);
-    __threadfence_block();
+    block_excl_scan<uint64_t>(c, sm.r64b, ctot);
+    *n_finite = ctot;
     __syncthreads();
     return tot;
+}
+
+// radix_select's query by value buckets (vsel_l1 must have run for this row).
+template <bool BF16, int VEC>
+__device__ __forceinline__ Sel vsel_query(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, float M,
+                                          double scale, int kind, uint64_t target, uint64_t excl, uint64_t excl_mass) {
+    constexpr int BPT = NVB / BLOCK;
+    const int tid = threadIdx.x;
+    const uint64_t* saved = a.row_hist + (int64_t)C.row * NVB * 2;
+    const float xs = excl != ~0ull ? key_s(excl) : -__builtin_inff();
+    const uint32_t xb = xs > -__builtin_inff() ? vbucket(xs, M) : 0xFFFFFFFFu;
+    uint64_t lc[BPT], lm[BPT], bc[BPT];
+    uint64_t rc = 0, rm = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; i++) {
+        const uint32_t b = (uint32_t)tid * BPT + i;
+        uint64_t m = saved[2 * b], c = saved[2 * b + 1];
+        if (b == xb) {  // the excluded element
+            c -= 1;
+            m -= excl_mass;
+        }
+        bc[i] = c;
+        rc += c;
+        rm += m;
+        lc[i] = rc;
+        lm[i] = rm;
+    }
+    uint64_t tc, tm;
+    const uint64_t pc = block_excl_scan<uint64_t>(rc, sm.r64, tc);
+    const uint64_t pm = block_excl_scan<uint64_t>(rm, sm.r64b, tm);
+    if (kind == 0 && target >= tc)  // among the -inf elements
+        return radix_select<BF16, VEC>(a, sm, C, P, M, scale, kind, target, excl, excl_mass);
+    uint32_t hit = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < BPT; i++) {
+        const bool ok = kind == 0 ? (pc + lc[i] > target) : (bc[i] > 0 && pm + lm[i] >= target);
+        if (hit == 0xFFFFFFFFu && ok) hit = (uint32_t)tid * BPT + i;
+    }
+    hit = block_min_u(hit, sm.ru);
+    if (hit == 0xFFFFFFFFu) {  // target beyond the total (rounding): the last non-empty bucket
+        uint32_t l = 0;
+#pragma unroll
+        for (int i = 0; i < BPT; i++)
+            if (bc[i] > 0) l = (uint32_t)tid * BPT + i + 1;
+        l = (uint32_t)block_max_u64(l, sm.r64);
+        hit = l ? l - 1 : 0;
+    }
+    if ((uint32_t)tid == hit / BPT) {
+        const int i = (int)(hit % BPT);
+        uint64_t cab = pc, mab = pm, nbk = 0;
+#pragma unroll
+        for (int ii = 0; ii < BPT; ii++) {
+            if (ii + 1 == i) {
+                cab = pc + lc[ii];
+                mab = pm + lm[ii];
+            }
+            if (ii == i) nbk = bc[ii];
+        }
+        sm.r64[0] = cab;
+        sm.r64b[0] = mab;
+        sm.r64[1] = nbk;
+    }
+    __syncthreads();
+    const uint64_t before_cnt = sm.r64[0], before_mass = sm.r64b[0], nbk = sm.r64[1];
+    __syncthreads();
+    if (nbk > (uint64_t)NMAX || nbk == 0)  // too dense to sort in LDS
+        return radix_select<BF16, VEC>(a, sm, C, P, M, scale, kind, target, excl, excl_mass);
+    // gather the bucket, sort it, walk it
+    if (tid == 0) sm.misc[MISC_N] = 0;
+    __syncthreads();
+    row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) __attribute__((always_inline)) {
+        if (!(s > -__builtin_inff()) || vbucket(s, M) != hit) return;
+        const uint64_t k = key64(s, id);
+        if (k == excl) return;
+        const uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+        if (slot < NMAX) sm.u.cb.keys[slot] = k;
+    });
+    __syncthreads();
+    const int N = (int)min(sm.misc[MISC_N], (uint32_t)NMAX);
+    if (N <= BLOCK && N > WAVE) sort_list_regs(sm, N);
+    else sort_list(sm, N);
+    uint64_t loc[PT];
+    uint64_t run = 0;
+#pragma unroll
+    for (int i = 0; i < PT; i++) {
+        const int j = tid * PT + i;
+        run += j < N ? efix_of(key_s(sm.u.cb.keys[j]), M, scale) : 0ull;
+        loc[i] = run;
+    }
+    uint64_t tot;
+    const uint64_t pre = block_excl_scan<uint64_t>(run, sm.r64, tot);
+    uint32_t best = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < PT; i++) {
+        const int j = tid * PT + i;
+        if (best != 0xFFFFFFFFu || j >= N) continue;
+        const bool ok = kind == 0 ? (before_cnt + (uint64_t)j >= target) : (before_mass + pre + loc[i] >= target);
+        if (ok) best = (uint32_t)j;
+    }
+    best = block_min_u(best, sm.ru);
+    if (best == 0xFFFFFFFFu) best = N > 0 ? (uint32_t)N - 1 : 0u;
+    if ((uint32_t)tid == best / PT) {
+        const int i = (int)(best % PT);
+        uint64_t li = 0;
+#pragma unroll
+        for (int ii = 0; ii < PT; ii++)
+            if (ii == i) li = loc[ii];
+        sm.r64[0] = sm.u.cb.keys[best];
+        sm.r64[1] = before_mass + pre + li;
+    }
+    __syncthreads();
+    Sel r;
+    r.key = sm.r64[0];
+    r.cum_mass = sm.r64[1];
+    r.pos = before_cnt + best;
+    __syncthreads();
+    return r;
 }
 
 // Rows the candidate lists do not cover, in sorted order: top-k / top-p / min-p cuts and
@@ -1618,7 +1748,8 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
     const double scale = ldexp(1.0, a.fix_bits);
     const uint64_t V = (uint64_t)a.V;
 
-    const uint64_t S_fix = radix_l1<BF16, VEC>(a, sm, C, P, M, scale);
+    uint64_t n_finite;
+    const uint64_t S_fix = vsel_l1<BF16, VEC>(a, sm, C, P, M, scale, &n_finite);
     const uint64_t Lk = C.kmode ? (uint64_t)C.k : V;
     uint64_t Lp = ~0ull, Lm = ~0ull, L = 0, T = 0, kept_mass = 0, kd = ~0ull, md = 0;
     Sel selp{0, 0, 0}, last{0, 0, 0};
@@ -1733,7 +1864,7 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
             ex = kd;
             exm = md;
         }
-        const Sel r = radix_select<BF16, VEC>(a, sm, C, P, M, scale, kind, target, ex, exm);
+        const Sel r = vsel_query<BF16, VEC>(a, sm, C, P, M, scale, kind, target, ex, exm);
         if (st == Q_K) {  // top-p runs over the top-k list: cut inside it, or keep all k
             if (r.cum_mass < T) {
                 Lp = Lk;
@@ -2027,8 +2158,10 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
     }
 }
 
+// One workgroup per row and usually one per CU: registers up to 256 per lane (two waves
+// per SIMD) rather than spills for a third.
 template <bool BF16>
-__global__ __launch_bounds__(BLOCK) void k_select(KArgs a) {
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_select(KArgs a) {
     __shared__ Smem sm;
     if (a.trace && threadIdx.x == 0)
         for (int i = 0; i < 8; i++) sm.tr[i] = 0;
