@@ -71,6 +71,18 @@ def compare_target(cfg, gpu, orc, logits_f32=None, check_list=True):
             if tok_g != tok_o:
                 problems.append(f"row {b}: token target gpu={tok_g} oracle={tok_o}")
             continue
+        # the softmax max is exact (x / T correctly rounded) and S within 2e-6 of an f64 sum
+        if "stats" in gpu and "stats" in orc and p["temperature"] > 0.0:
+            gm, om = np.float32(gpu["stats"][b, 0]), np.float32(orc["stats"][b, 0])
+            if np.isfinite(om) and gm.view(np.uint32) != om.view(np.uint32):
+                problems.append(f"row {b}: max gpu={gm!r} oracle={om!r}")
+                continue
+            if np.isfinite(om) and orc.get("s") is not None:
+                sv = orc["s"][b].astype(np.float64)
+                s_ex = float(np.sum(np.exp(sv[np.isfinite(sv)] - float(om))))
+                if abs(float(gpu["stats"][b, 1]) - s_ex) > 2e-6 * s_ex:
+                    problems.append(f"row {b}: sum gpu={float(gpu['stats'][b, 1])!r} f64={s_ex!r}")
+                    continue
         kl_o, kl_g = int(orc["kept_len"][b]), int(gpu["kept_len"][b])
         band = False
         if kl_o != kl_g:
