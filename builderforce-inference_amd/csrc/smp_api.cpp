@@ -268,7 +268,7 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     a.bm_words = bm_words;
     a.trace = nullptr;
     if (ctx->tracing) {
-        size_t words = ((size_t)c.n_rows * s.n_chunks + (size_t)c.n_rows) * 8;
+        size_t words = (size_t)c.n_rows * s.n_chunks * 8 + (size_t)c.n_rows * 16;
         if (words > ctx->trace_words) {
             if (ctx->trace) (void)hipFree(ctx->trace);
             ctx->trace = nullptr;

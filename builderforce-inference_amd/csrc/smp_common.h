@@ -23,10 +23,47 @@ struct RowCtx {
     bool greedy, kmode, pmode, mmode;
     Pen pen;
     bool pen_on;
+    // prepen: the stream pass applies the penalties (history of at most PREPEN_H ids), so
+    // its chunk results and candidates are penalized; pen_hash: the select kernel keeps the
+    // history in its LDS hash and corrects the chunk results itself
+    bool prepen, pen_hash;
     HistView h;
     const uint32_t* mrow;
     const char* lrow;
 };
+
+// A row-uniform read of memory the kernels never write (parameters, offsets, uniforms,
+// drafts): through the constant address space it becomes a scalar load, so nothing waits
+// for it behind the logits' vector loads.
+template <typename T>
+__device__ __forceinline__ T ld_uniform(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)p;
+}
+
+// The history of a row (sample.rs:345-367 `prev`): its base ids, plus for spec verify the
+// drafts before this row (spec.rs:137-162 appends each accepted draft). Reads only the
+// row's two history offsets.
+__device__ __forceinline__ HistView row_history(const KArgs& a, int row) {
+    HistView h;
+    const int rps = a.rows_per_seq;
+    const int seq = rps > 0 ? row / rps : row;
+    if (rps > 0) {
+        h.extra = a.drafts + (int64_t)seq * (rps - 1);
+        h.nextra = row % rps;
+    } else {
+        h.extra = nullptr;
+        h.nextra = 0;
+    }
+    if (a.hist_off) {
+        const int64_t o0 = ld_uniform(a.hist_off + seq), o1 = ld_uniform(a.hist_off + seq + 1);
+        h.base = a.hist + o0;
+        h.nbase = o1 > o0 ? o1 - o0 : 0;
+    } else {
+        h.base = nullptr;
+        h.nbase = 0;
+    }
+    return h;
+}
 
 __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
     RowCtx C;
@@ -36,22 +73,20 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
         int rps = a.rows_per_seq;
         C.seq = row / rps;
         C.ri = row % rps;
-        int dl = a.draft_len[C.seq];
+        int dl = ld_uniform(a.draft_len + C.seq);
         dl = dl < 0 ? 0 : (dl > rps - 1 ? rps - 1 : dl);
         C.dl = dl;
         C.active = C.ri <= dl;
         C.judged = C.ri < dl;
         const int64_t dbase = (int64_t)C.seq * (rps - 1);
-        C.draft = C.judged ? a.drafts[dbase + C.ri] : 0u;
+        C.draft = C.judged ? ld_uniform(a.drafts + dbase + C.ri) : 0u;
         if (C.judged) {
-            C.u = a.u_pairs[(dbase + C.ri) * 2];
-            C.u2 = a.u_pairs[(dbase + C.ri) * 2 + 1];
+            C.u = ld_uniform(a.u_pairs + (dbase + C.ri) * 2);
+            C.u2 = ld_uniform(a.u_pairs + (dbase + C.ri) * 2 + 1);
         } else {
-            C.u = a.u_bonus[C.seq];
+            C.u = ld_uniform(a.u_bonus + C.seq);
             C.u2 = 0.0f;
         }
-        C.h.extra = a.drafts + dbase;
-        C.h.nextra = C.ri;
     } else {
         C.seq = row;
         C.ri = 0;
@@ -59,20 +94,22 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
         C.active = true;
         C.judged = false;
         C.draft = 0;
-        C.u = a.u ? a.u[row] : 0.0f;
+        C.u = a.u ? ld_uniform(a.u + row) : 0.0f;
         C.u2 = 0.0f;
-        C.h.extra = nullptr;
-        C.h.nextra = 0;
     }
-    const bfi_smp_row_params P = a.params[C.seq];
-    if (a.hist_off) {
-        int64_t o0 = a.hist_off[C.seq], o1 = a.hist_off[C.seq + 1];
-        C.h.base = a.hist + o0;
-        C.h.nbase = o1 > o0 ? o1 - o0 : 0;
-    } else {
-        C.h.base = nullptr;
-        C.h.nbase = 0;
-    }
+    C.h = row_history(a, row);
+    // field by field: an aggregate copy would lose the address space
+    const __attribute__((address_space(4))) uint32_t* pw =
+        (const __attribute__((address_space(4))) uint32_t*)(a.params + C.seq);
+    bfi_smp_row_params P;
+    P.temperature = __uint_as_float(pw[0]);
+    P.top_k = (int32_t)pw[1];
+    P.top_p = __uint_as_float(pw[2]);
+    P.min_p = __uint_as_float(pw[3]);
+    P.repeat_penalty = __uint_as_float(pw[4]);
+    P.presence_penalty = __uint_as_float(pw[5]);
+    P.frequency_penalty = __uint_as_float(pw[6]);
+    P.reserved = pw[7];
     const int64_t H = C.h.size();
     C.T = P.temperature;
     C.rT = 1.0f / P.temperature;  // IEEE, once per row
@@ -93,6 +130,8 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
     C.pen.pres_on = P.presence_penalty != 0.0f && H > 0;               // sample.rs:360
     C.pen.freq_on = P.frequency_penalty != 0.0f && H > 0;
     C.pen_on = C.pen.rep_on || C.pen.pres_on || C.pen.freq_on;
+    C.prepen = C.pen_on && H <= (int64_t)PREPEN_H && (C.greedy || C.stream_ok) && a.chunk <= CHUNK_MAX;
+    C.pen_hash = C.pen_on && !C.prepen;
     C.mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
     const int esz = 4;  // overridden by the loader for bf16
     (void)esz;
@@ -135,6 +174,23 @@ __device__ __forceinline__ void unpack16(const uint4 w, float (&v)[Elem<BF16>::E
             v[2 * e + 1] = __uint_as_float(ww[e] & 0xFFFF0000u);
         }
     }
+}
+
+// A full, aligned tile: the VEC 16-byte loads are issued in order (q = 0 first), so a
+// consumer that walks q upward waits only for the vectors it needs.
+template <bool BF16, int VEC>
+__device__ __forceinline__ void load_full_tile(const KArgs& a, int row, uint32_t c0,
+                                               float (&x)[VEC][Elem<BF16>::EPV]) {
+    typedef typename Elem<BF16>::T T;
+    const T* base = (const T*)a.logits + (int64_t)row * a.row_stride + c0 + (uint32_t)threadIdx.x * Elem<BF16>::EPV;
+    uint4 w[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; q++) {
+        w[q] = *(const uint4*)(base + (uint32_t)(q * BLOCK) * Elem<BF16>::EPV);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = 0; q < VEC; q++) unpack16<BF16, VEC>(w[q], x[q]);
 }
 
 template <bool BF16, int VEC>

@@ -22,6 +22,7 @@ constexpr int WAVE = 64;
 constexpr int NWAVE = BLOCK / WAVE;
 constexpr int CHUNK_MAX = 8192;        // logits elements per workgroup (stream phase)
 constexpr int NCMAX = 256;             // chunks per row
+constexpr int PREPEN_H = 1024;         // histories up to this length are applied by the stream pass
 constexpr int CAND_CAP = 2048;         // candidates one chunk may hand to the combine
 constexpr int NMAX = 2048;             // combine sort capacity (power of two)
 constexpr int NBUCKET = 1024;          // radix buckets (10-bit key digits) of the fallback select
@@ -36,21 +37,23 @@ constexpr uint32_t NCAND_UNBOUNDED = 0xFFFFFFFFu;  // row has no top-k / min-p b
 constexpr uint32_t NCAND_OVERFLOW = 0xFFFFFFFEu;   // chunk had more than CAND_CAP candidates
 constexpr float F32_EPS = 1.1920928955078125e-07f;  // f32::EPSILON
 
-// Per (row, chunk) result of the streaming pass over un-penalized values s = masked x / T
-// (greedy: the masked logits).
+// Per (row, chunk) result of the streaming pass over the values s = x / T of the masked
+// logits x (greedy: x itself), penalized when the row's context says prepen (else the
+// select kernel corrects the history ids).
 struct ChunkPart {
     float m;          // max of s (exact)
     uint32_t arg;     // greedy: first index attaining m
     double sum;       // sum of stream_term over the chunk (f64 over per-vector f32 sums)
     uint32_t ncand;   // candidates written, or NCAND_UNBOUNDED / NCAND_OVERFLOW
     float theta;      // every element of the chunk with finite s >= theta was written
-    float raw_m;      // max of the masked logits (the terms' reference point)
-    uint32_t raw_arg; // its first index (greedy rows and rows with min_p > 1)
+    float raw_m;      // max of x (the terms' reference point); rows with min_p > 1: of the
+                      // un-penalized masked logits
+    uint32_t raw_arg; // first index of that maximum (greedy rows and rows with min_p > 1)
     uint32_t pad;
     uint32_t pad2;
 };
 
-// A candidate of the kept set: its index and masked logit (the select kernel divides by T).
+// A candidate of the kept set: its index and x (the select kernel divides by T).
 struct Cand {
     uint32_t idx;
     float x;
@@ -426,7 +429,7 @@ __device__ __forceinline__ ArgMax argmax_merge(ArgMax a, ArgMax b) {
     if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
     return a;
 }
-__device__ __forceinline__ ArgMax block_argmax(ArgMax a, float* scrv, uint32_t* scri) {
+__device__ __forceinline__ ArgMax wave_argmax(ArgMax a) {
     // (value, index) packed in 64 bits for the DPP scan; merged with argmax_merge
     const uint64_t packed = ((uint64_t)__float_as_uint(a.v) << 32) | a.i;
     const uint64_t ident = ((uint64_t)__float_as_uint(-__builtin_inff()) << 32) | 0xFFFFFFFFu;
@@ -435,7 +438,10 @@ __device__ __forceinline__ ArgMax block_argmax(ArgMax a, float* scrv, uint32_t* 
                                       ArgMax{__uint_as_float((uint32_t)(y >> 32)), (uint32_t)y});
         return ((uint64_t)__float_as_uint(m.v) << 32) | m.i;
     }));
-    a = ArgMax{__uint_as_float((uint32_t)(r64 >> 32)), (uint32_t)r64};
+    return ArgMax{__uint_as_float((uint32_t)(r64 >> 32)), (uint32_t)r64};
+}
+__device__ __forceinline__ ArgMax block_argmax(ArgMax a, float* scrv, uint32_t* scri) {
+    a = wave_argmax(a);
     if (lane_id() == 0) {
         scrv[wave_id()] = a.v;
         scri[wave_id()] = a.i;

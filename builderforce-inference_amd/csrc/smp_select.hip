@@ -66,7 +66,7 @@ struct __align__(16) Smem {
     uint64_t r64[NWAVE];
     uint64_t r64b[NWAVE];
     uint32_t misc[8];
-    uint64_t tr[8];  // phase timestamps of this workgroup (diagnostics)
+    uint64_t tr[16];  // phase timestamps of this workgroup (diagnostics)
     // row aggregates built with LDS atomics (integer, so independent of the order)
     struct {
         uint64_t gkey;    // greedy: max over (value, index) keys (argmax_key)
@@ -180,7 +180,7 @@ __device__ __forceinline__ bool hist_build(const KArgs& a, Smem& sm, const RowCt
         sm.hcnt[k] = 0;
     }
     if (tid == 0) sm.misc[MISC_HN] = 0;
-    const int64_t H = C.pen_on ? C.h.size() : 0;
+    const int64_t H = C.pen_hash ? C.h.size() : 0;
     const uint32_t V = (uint32_t)a.V;
     ho.regs = H <= (int64_t)HB * BLOCK;
     ho.own = 0;
@@ -405,7 +405,7 @@ __device__ __forceinline__ void span_pass(const KArgs& a, const Smem& sm, const 
                 const uint32_t id = id0 + e;
                 if (id >= t1) continue;
                 if (SKIP_HIST) {
-                    if (C.pen_on && hist_find(sm, id) >= 0) continue;
+                    if (C.pen_hash && hist_find(sm, id) >= 0) continue;
                     f(id, raw_value(C, x[q][e], (mb >> e) & 1u));
                 } else {
                     f(id, x[q][e]);
@@ -671,6 +671,7 @@ template <int E>
 __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const RowCtx& C, int N, bool sorted, float M,
                                              float S, ArgMax rawmax, bool exhaustive, bool minp_complete) {
     enum { R_TOK = 0, R_VERDICT = 1, R_KIND = 2 };  // R_KIND: 0 weights, 1 token target, 2 undecided
+    BFI_TRACE(a, 0, 13);
     if (wave_id() == 0) {
         const int lane = lane_id();
         bool valid[E];
@@ -818,9 +819,11 @@ __device__ __forceinline__ bool combine_wave(const KArgs& a, Smem& sm, const Row
             sm.misc[4 + R_KIND] = kind;
         }
     }
+    BFI_TRACE(a, 0, 14);
     __syncthreads();
     const uint32_t tok = sm.misc[4 + R_TOK], verdict = sm.misc[4 + R_VERDICT], kind = sm.misc[4 + R_KIND];
     __syncthreads();
+    BFI_TRACE(a, 0, 15);
     if (kind == 2) return false;
     if (kind == 1) {
         finish_token(a, sm, C, tok);
@@ -1005,22 +1008,32 @@ __device__ __forceinline__ CandBatch load_cands(const KArgs& a, const Smem& sm, 
     const uint32_t tot = sm.cpre[nc];
     const Cand* cands = a.cands + (int64_t)row * nc * CAND_CAP;
     const uint32_t f0 = b0 + threadIdx.x;
-    CandBatch B;
-    int lo = 0, hi = nc;  // chunk of f0: largest c with cpre[c] <= f0
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (sm.cpre[mid] <= f0) lo = mid;
-        else hi = mid;
+    // the chunk of each f: the largest c < nc with cpre[c] <= f, by GU binary searches
+    // whose LDS reads are independent (their latencies overlap)
+    int lo[GU];
+#pragma unroll
+    for (int g = 0; g < GU; g++) lo[g] = 0;
+    int top = 1;
+    while (top * 2 < nc) top *= 2;
+    for (int st = top; st > 0; st >>= 1) {
+#pragma unroll
+        for (int g = 0; g < GU; g++) {
+            // c >= nc reads cpre[nc] = the total, which no f < total passes (an f beyond
+            // the total loads nothing); no branch, so the GU reads go out together
+            const int c = min(lo[g] + st, nc);
+            lo[g] = sm.cpre[c] <= f0 + g * BLOCK ? c : lo[g];
+        }
     }
+    uint32_t start[GU];
+#pragma unroll
+    for (int g = 0; g < GU; g++) start[g] = sm.cpre[lo[g]];
+    CandBatch B;
 #pragma unroll
     for (int g = 0; g < GU; g++) {
         const uint32_t f = f0 + g * BLOCK;
         B.cd[g].idx = 0;
         B.cd[g].x = -__builtin_inff();
-        if (f < tot) {
-            while (sm.cpre[lo + 1] <= f) lo++;  // f only grows
-            B.cd[g] = cands[(int64_t)lo * CAND_CAP + (f - sm.cpre[lo])];
-        }
+        if (f < tot) B.cd[g] = cands[(int64_t)lo[g] * CAND_CAP + (f - start[g])];
     }
     return B;
 }
@@ -1033,7 +1046,7 @@ __device__ __forceinline__ void append_cands(Smem& sm, const RowCtx& C, const Ca
 #pragma unroll
     for (int g = 0; g < GU; g++) {
         v[g] = raw_value(C, B.cd[g].x, true);  // masked logit / T, exact
-        if (v[g] >= th && v[g] > -__builtin_inff() && !(C.pen_on && hist_find(sm, B.cd[g].idx) >= 0))
+        if (v[g] >= th && v[g] > -__builtin_inff() && !(C.pen_hash && hist_find(sm, B.cd[g].idx) >= 0))
             take |= 1u << g;
     }
     // one reservation per wave for all its entries
@@ -1059,7 +1072,7 @@ __device__ __forceinline__ void append_cands(Smem& sm, const RowCtx& C, const Ca
 
 // Appends the history ids whose penalized value is >= th. Every thread calls it.
 __device__ __forceinline__ void append_hist(Smem& sm, const RowCtx& C, float th, bool sorted) {
-    if (!C.pen_on) return;
+    if (!C.pen_hash) return;
     const int nh = (int)sm.misc[MISC_HN];
     for (int j0 = 0; j0 < nh; j0 += BLOCK) {  // uniform trip count: wave_append below
         const int j = j0 + threadIdx.x;
@@ -1101,11 +1114,11 @@ __device__ __forceinline__ float topk_bound(const KArgs& a, Smem& sm, const RowC
 #pragma unroll
         for (int g = 0; g < GU; g++) {
             const float v = raw_value(C, B.cd[g].x, true);
-            if (v >= th && v > -__builtin_inff() && !(C.pen_on && hist_find(sm, B.cd[g].idx) >= 0))
+            if (v >= th && v > -__builtin_inff() && !(C.pen_hash && hist_find(sm, B.cd[g].idx) >= 0))
                 lds_add(&cnt[bucket(v)], 1u);
         }
     }
-    if (C.pen_on) {
+    if (C.pen_hash) {
         for (int j = tid; j < (int)sm.misc[MISC_HN]; j += BLOCK) {
             const float v = sm.hpen[sm.hlist[j]];
             if (v >= th && v > -__builtin_inff()) lds_add(&cnt[bucket(v)], 1u);
@@ -1133,17 +1146,19 @@ __device__ __forceinline__ float topk_bound(const KArgs& a, Smem& sm, const RowC
 
 // `th_raw`: every non-history element >= th_raw is some chunk's candidate (the largest chunk
 // bound). `list_ready`: the first pass's list (complete above max(th_raw, min-p bound)) is
-// already in sm.u.cb.keys with its length in MISC_N.
-template <bool BF16, int VEC>
+// already in sm.u.cb.keys with its length in MISC_N. `need_hash()` runs before the second
+// pass, whose chunk re-reads take the penalties from the LDS history hash.
+template <bool BF16, int VEC, typename F>
 __device__ __forceinline__ int combine_bounded(const KArgs& a, Smem& sm, const RowCtx& C, const ChunkPart& mine,
                                                float M, float S, ArgMax rawmax, float th_raw, bool list_ready,
-                                               int64_t tb) {
+                                               int64_t tb, F need_hash) {
     const int tid = threadIdx.x;
     const int nc = a.n_chunks;
     const bool sorted = C.kmode || C.pmode;  // else min-p only: index order (sample.rs:411-414)
     const float th_m = minp_bound(C, M);
     float th = fmaxf(th_raw, th_m);
     for (int pass = 0; pass < 2; pass++) {
+        if (pass) need_hash();
         // ---- the list: complete above th
         if (!(pass == 0 && list_ready)) {
             chunk_prefix(sm, nc, tid < nc ? chunk_take(mine, th) : 0u);
@@ -1290,7 +1305,7 @@ __device__ __forceinline__ float element_s(const KArgs& a, Smem& sm, const RowCt
     const bool allowed = !C.mrow || ((C.mrow[id >> 5] >> (id & 31)) & 1u);
     uint32_t c = 0;
     if (C.pen_on) {
-        if (hashed) {
+        if (hashed && C.pen_hash) {
             const int k = hist_find(sm, id);
             c = k >= 0 ? sm.hcnt[k] : 0u;
         } else {
@@ -1964,8 +1979,9 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
     const int64_t tb = 0;
     BFI_TRACE(a, tb, 0);
     if (row >= a.n_rows) return;
-    const RowCtx C = make_ctx(a, row);
+    RowCtx C = make_ctx(a, row);
     if (!C.active) return;
+    BFI_TRACE(a, tb, 8);
     const bool track_raw = !C.greedy && C.min_p > 1.0f;
     const bool cand_row = !C.greedy && (C.kmode || C.pmode || C.mmode);  // may have candidate lists
 
@@ -2001,6 +2017,7 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
     }
     HistOwn ho;
     const bool hashed = hist_build<BF16>(a, sm, C, ho, [&]() {
+        BFI_TRACE(a, tb, 9);
         if (tid < nc) {
             sm.cm[tid] = mine.m;
             sm.cxm[tid] = mine.raw_m;
@@ -2018,6 +2035,7 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
         // prefix over every chunk's candidate list (the first pass filters them later)
         if (cand_row) chunk_prefix(sm, nc, tid < nc && mine.ncand <= (uint32_t)CAND_CAP ? mine.ncand : 0u);
         if (tid == 0) sm.misc[MISC_N] = 0;
+        BFI_TRACE(a, tb, 10);
     });
     BFI_TRACE(a, tb, 1);
     // bounded rows: the first candidate loads go out now and land during the history work
@@ -2025,9 +2043,21 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
     const bool bounded = cand_row && hashed && C.stream_ok && sm.ag.flags == 0u;
     CandBatch first;
     if (bounded) first = load_cands(a, sm, row, nc, 0);
+    BFI_TRACE(a, tb, 2);
     // masked, un-penalized argmax (min-p fallback, sample.rs:415-422)
     const ArgMax rawmax = track_raw ? argmax_of_key(sm.ag.rawkey) : ArgMax{-__builtin_inff(), 0xFFFFFFFFu};
     const PenSrc H{true, nullptr, nullptr, nullptr};
+    // Rows whose penalties the stream pass applied have an empty hash; the passes that
+    // re-read logits (repairs, index-order draws) build it first. Its values do not change
+    // M or S, which are final by then.
+    auto need_hash = [&]() __attribute__((always_inline)) {
+        if (C.prepen && !C.pen_hash) {
+            C.pen_hash = true;
+            HistOwn h2;
+            hist_build<BF16>(a, sm, C, h2, []() {});
+            hist_values(a, sm, C, h2);
+        }
+    };
     const int nw = a.bm_words;
     const uint32_t* gbm = a.row_pen + (int64_t)row * (2 * nw + GDCAP);
     const PenSrc GT{false, gbm, gbm + nw, gbm + 2 * nw};
@@ -2044,7 +2074,7 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
     } else {
         // ---- B: history values (sample.rs:331-375) and the streaming terms they replace
         uint32_t dirty = 0;
-        if (C.pen_on) {
+        if (C.pen_hash) {
             hist_values(a, sm, C, ho);
             if (sm.ag.nd) {
                 // rare: a chunk whose maximum is a history id; re-read it for the max and
@@ -2089,7 +2119,6 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
                 __syncthreads();
             }
         }
-        BFI_TRACE(a, tb, 2);
         if (C.greedy) {  // sample.rs:369-371, 429-439
             const ArgMax am = argmax_of_key(sm.ag.gkey);
             finish_token(a, sm, C, am.v > -__builtin_inff() ? am.i : 0u);
@@ -2104,7 +2133,7 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
         // 2^-44 fixed point) and, for bounded rows, the candidate prefix of the first pass
         constexpr double FIX44 = 17592186044416.0;
         uint64_t sf = 0;  // this thread's share of S, fixed point
-        if (C.pen_on) {
+        if (C.pen_hash) {
             for (int j = tid; j < (int)sm.misc[MISC_HN]; j += BLOCK) {
                 const int k = sm.hlist[j];
                 const uint32_t c = sm.hkey[k] / (uint32_t)a.chunk;
@@ -2114,7 +2143,7 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
             }
         }
         if (tid < nc && mine.m > -__builtin_inff()) {
-            const double rc = mine.sum - (C.pen_on && !dirty ? (double)sm.craw[tid] / FIX52 : 0.0);
+            const double rc = mine.sum - (C.pen_hash && !dirty ? (double)sm.craw[tid] / FIX52 : 0.0);
             wc = rc * (double)expf(mine.m - M);
             sf += (uint64_t)(wc * FIX44);
         }
@@ -2123,14 +2152,16 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
         if (bounded) {  // the first pass's list: complete above max(th_raw, min-p bound)
             const float th = fmaxf(th_raw, minp_bound(C, M));
             const bool sorted = C.kmode || C.pmode;
+            BFI_TRACE(a, tb, 11);
             append_cands(sm, C, first, th, sorted);
+            BFI_TRACE(a, tb, 12);
             for (uint32_t b0 = GU * BLOCK; b0 < sm.cpre[nc]; b0 += GU * BLOCK)  // uniform trip count
                 append_cands(sm, C, load_cands(a, sm, row, nc, b0), th, sorted);
             append_hist(sm, C, th, sorted);
         }
         __syncthreads();
         S = (float)((double)sm.ag.sfix / FIX44);
-        if (tid < nc && C.pen_on) wc += (double)sm.cpen[tid] / FIX52;
+        if (tid < nc && C.pen_hash) wc += (double)sm.cpen[tid] / FIX52;
         BFI_TRACE(a, tb, 3);
         if (a.t_stats && tid == 0) {
             a.t_stats[row * 4 + 0] = M;
@@ -2138,7 +2169,8 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
             a.t_stats[row * 4 + 3] = unfiltered ? 2.0f : (bounded ? 1.0f : 3.0f);
         }
         if (bounded) {
-            if (combine_bounded<BF16, VEC>(a, sm, C, mine, M, S, rawmax, th_raw, true, tb) == CB_DONE) return;
+            if (combine_bounded<BF16, VEC>(a, sm, C, mine, M, S, rawmax, th_raw, true, tb, need_hash) == CB_DONE)
+                return;
             if (a.t_stats && tid == 0) a.t_stats[row * 4 + 3] = 3.0f;
         }
         route = (C.kmode || C.pmode) ? R_RADIX : R_INDEX;
@@ -2148,6 +2180,7 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
         a.t_stats[row * 4 + 1] = S;
     }
     const bool full = !hashed || !C.stream_ok;  // the global history tables are built
+    if (!full) need_hash();
     if (route == R_RADIX) {
         if (!full) build_row_pen(a, sm, C);
         combine_radix<BF16, VEC>(a, sm, C, GT, hashed, M, S, rawmax);
@@ -2158,19 +2191,125 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
     }
 }
 
+// ---- fast finish ------------------------------------------------------------------------
+//
+// The common row, first and on short code (three barriers): every chunk handed over a
+// candidate list, penalties (if any) were applied by the stream pass, and the list above
+// the row's bound holds at most 8 * WAVE entries. One wave forms the row aggregates from
+// the chunk results with DPP (no LDS round trips), the block gathers the list, one wave
+// sorts and draws (combine_wave, as the general path's first pass). Returns false for any
+// other row, which then starts over on the general path (select_row).
+template <bool BF16>
+__device__ __forceinline__ bool select_fast(const KArgs& a, Smem& sm, int row) {
+    const int tid = threadIdx.x, lane = lane_id();
+    const int nc = a.n_chunks;
+    if (nc > WAVE) return false;
+    // the chunk results go out before the row's parameters: the two latencies overlap
+    ChunkPart mine;
+    mine.m = -__builtin_inff();
+    mine.sum = 0.0;
+    mine.arg = 0xFFFFFFFFu;
+    mine.ncand = 0;
+    mine.theta = -__builtin_inff();
+    mine.raw_m = -__builtin_inff();
+    mine.raw_arg = 0xFFFFFFFFu;
+    if (tid < nc) mine = a.parts[(int64_t)row * nc + tid];
+    const RowCtx C = make_ctx(a, row);
+    if (!C.active) return true;  // a verify row past its draft: nothing to emit
+    BFI_TRACE(a, 0, 8);
+    const bool cand_row = C.kmode || C.pmode || C.mmode;
+    if (C.pen_hash || !(C.greedy || (cand_row && C.stream_ok))) return false;
+    const bool sorted = C.kmode || C.pmode;  // else min-p only: index order (sample.rs:411-414)
+    enum { F_STATUS = 0, F_TOK = 1, F_M = 2, F_S = 3, F_TH = 4, F_THM = 5, F_RAWV = 6, F_RAWI = 7 };
+    uint32_t* fx = reinterpret_cast<uint32_t*>(sm.ru);  // NWAVE >= 8 words
+    if (wave_id() == 0) {
+        const bool in = lane < nc;
+        uint32_t status = 0;  // 0: list, 1: token (greedy), 2: leave to k_select
+        if (C.greedy) {  // sample.rs:369-371, 429-439: argmax of the penalized logits
+            const ArgMax am = argmax_of_key(wave_max_u64(in ? argmax_key(mine.m, mine.arg) : 0ull));
+            status = 1;
+            if (lane == 0) fx[F_TOK] = am.v > -__builtin_inff() ? am.i : 0u;
+        } else {
+            const bool open = in && (mine.ncand == NCAND_UNBOUNDED || mine.ncand == NCAND_OVERFLOW);
+            const float M = wave_max(in ? mine.m : -__builtin_inff());
+            if (__ballot(open) || !(M > -__builtin_inff())) {
+                status = 2;
+            } else {
+                // S: the chunks' sums moved to the row max (sample.rs:376-386)
+                const double wc = in && mine.m > -__builtin_inff() ? mine.sum * (double)expf(mine.m - M) : 0.0;
+                const float S = (float)wave_sum_d(wc);
+                const float th_m = minp_bound(C, M);
+                const float th = fmaxf(wave_max(in ? mine.theta : -__builtin_inff()), th_m);
+                const uint32_t take = in ? chunk_take(mine, th) : 0u;
+                const uint32_t incl = wave_scan_incl(take, 0u, [](uint32_t x, uint32_t y) { return x + y; });
+                if (in) sm.cpre[lane] = incl - take;
+                const ArgMax rawmax = C.min_p > 1.0f
+                    ? argmax_of_key(wave_max_u64(in ? argmax_key(mine.raw_m, mine.raw_arg) : 0ull))
+                    : ArgMax{-__builtin_inff(), 0xFFFFFFFFu};
+                if (lane == 0) {
+                    sm.cpre[nc] = lane63(incl);
+                    fx[F_M] = __float_as_uint(M);
+                    fx[F_S] = __float_as_uint(S);
+                    fx[F_TH] = __float_as_uint(th);
+                    fx[F_THM] = __float_as_uint(th_m);
+                    fx[F_RAWV] = __float_as_uint(rawmax.v);
+                    fx[F_RAWI] = rawmax.i;
+                    sm.misc[MISC_N] = 0;
+                }
+            }
+        }
+        if (lane == 0) fx[F_STATUS] = status;
+    }
+    __syncthreads();
+    BFI_TRACE(a, 0, 1);
+    const uint32_t status = fx[F_STATUS];
+    if (status == 1) {
+        finish_token(a, sm, C, fx[F_TOK]);
+        return true;
+    }
+    if (status == 2) return false;
+    const float M = __uint_as_float(fx[F_M]), S = __uint_as_float(fx[F_S]);
+    const float th = __uint_as_float(fx[F_TH]), th_m = __uint_as_float(fx[F_THM]);
+    const ArgMax rawmax{__uint_as_float(fx[F_RAWV]), fx[F_RAWI]};
+    for (uint32_t b0 = 0; b0 < sm.cpre[nc]; b0 += GU * BLOCK)  // uniform trip count
+        append_cands(sm, C, load_cands(a, sm, row, nc, b0), th, sorted);
+    __syncthreads();
+    BFI_TRACE(a, 0, 3);
+    if (a.t_stats && tid == 0) {
+        a.t_stats[row * 4 + 0] = M;
+        a.t_stats[row * 4 + 1] = S;
+        a.t_stats[row * 4 + 3] = 1.0f;
+    }
+    const int N = (int)sm.misc[MISC_N];
+    if (a.trace && tid == 0) sm.tr[6] = ((uint64_t)sm.cpre[nc] << 32) | (uint32_t)N;
+    const bool exhaustive = !(th > -__builtin_inff());
+    const bool minp_complete = th <= th_m;
+    if (N <= WAVE) return combine_wave<1>(a, sm, C, N, sorted, M, S, rawmax, exhaustive, minp_complete);
+    if (N > 8 * WAVE) return false;
+    sort_list_regs(sm, N);
+    BFI_TRACE(a, 0, 5);
+    return combine_wave<8>(a, sm, C, N, sorted, M, S, rawmax, exhaustive, minp_complete);
+}
+
 // One workgroup per row and usually one per CU: registers up to 256 per lane (two waves
-// per SIMD) rather than spills for a third.
+// per SIMD) rather than spills for a third. The fast finish goes first; a row it leaves
+// starts over on the general path.
 template <bool BF16>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_select(KArgs a) {
     __shared__ Smem sm;
     if (a.trace && threadIdx.x == 0)
-        for (int i = 0; i < 8; i++) sm.tr[i] = 0;
-    select_row<BF16>(a, sm);
+        for (int i = 0; i < 16; i++) sm.tr[i] = 0;
+    BFI_TRACE(a, 0, 0);
     const int row = select_row_id();
+    if (row >= a.n_rows) return;
+    if (!select_fast<BF16>(a, sm, row)) {
+        __syncthreads();
+        select_row<BF16>(a, sm);
+    }
     if (a.trace && threadIdx.x == 0 && row < a.n_rows) {
         sm.tr[7] = wall_clock64();
-        uint64_t* t = a.trace + ((int64_t)a.n_rows * a.n_chunks + row) * 8;
-        for (int i = 0; i < 8; i++) t[i] = sm.tr[i];
+        uint64_t* t = a.trace + (int64_t)a.n_rows * a.n_chunks * 8 + (int64_t)row * 16;
+        for (int i = 0; i < 16; i++) t[i] = sm.tr[i];
     }
 }
 
