@@ -24,7 +24,7 @@ struct bfi_smp_ctx {
     std::string err;
     char* ws = nullptr;  // parts | cands | row_res | row_pen | row_hist
     size_t ws_size = 0;
-    uint32_t* ctr = nullptr;  // row_ctr | seq_ctr, kept zero between launches
+    uint32_t* ctr = nullptr;  // seq_ctr, kept zero between launches
     size_t ctr_words = 0;
     bool ctr_dirty = false;
     // staging for bfi_smp_sample_host
@@ -222,7 +222,7 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     if (!choose_shape(c.n_rows, c.V, c.dtype == BFI_SMP_BF16, s))
         return fail(ctx, BFI_SMP_EINVAL, "no launch shape for n_vocab %lld", (long long)c.V);
     const Layout L = layout(c.n_rows, s, bm_words);
-    const size_t ctr_words = (size_t)c.n_rows + (size_t)(verify ? c.n_seq : 0);
+    const size_t ctr_words = verify ? (size_t)c.n_seq : 1;
     int rc = ensure_ws(ctx, L.total, ctr_words, stream);
     if (rc) return rc;
 
@@ -263,8 +263,7 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     a.row_res = (uint32_t*)(ctx->ws + L.row_res);
     a.row_pen = (uint32_t*)(ctx->ws + L.row_pen);
     a.row_hist = (uint64_t*)(ctx->ws + L.row_hist);
-    a.row_ctr = ctx->ctr;
-    a.seq_ctr = ctx->ctr + c.n_rows;
+    a.seq_ctr = ctx->ctr;
     a.bm_words = bm_words;
     a.trace = nullptr;
     if (ctx->tracing) {

@@ -95,7 +95,6 @@ struct KArgs {
     // workspace
     ChunkPart* parts;
     Cand* cands;
-    uint32_t* row_ctr;
     uint32_t* seq_ctr;
     uint32_t* row_res;   // verify: 2 words per row {verdict, token}
     uint32_t* row_pen;   // fallback select: per row bm[bm_words] + pre[bm_words] + cnt[GDCAP]
