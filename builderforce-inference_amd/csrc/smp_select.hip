@@ -1064,7 +1064,7 @@ __device__ __forceinline__ Sel radix_select(const KArgs& a, Smem& sm, const RowC
     int pbits = 0;
     uint64_t before_cnt = 0, before_mass = 0;
     (void)excl_mass;
-    for (int level = 0;; level++) {
+    for (;;) {  // one 10-bit digit of the key per round
         const int w = (64 - pbits) >= 10 ? 10 : 64 - pbits;
         const int shift = 64 - pbits - w;
         const uint32_t nb = 1u << w;
