@@ -176,21 +176,26 @@ __device__ __forceinline__ void unpack16(const uint4 w, float (&v)[Elem<BF16>::E
     }
 }
 
-// A full, aligned tile: the VEC 16-byte loads are issued in order (q = 0 first), so a
-// consumer that walks q upward waits only for the vectors it needs.
-template <bool BF16, int VEC>
-__device__ __forceinline__ void load_full_tile(const KArgs& a, int row, uint32_t c0,
-                                               float (&x)[VEC][Elem<BF16>::EPV]) {
+// Vectors [Q0, Q1) of a full, aligned tile: the 16-byte loads are issued in order (q = Q0
+// first), so a consumer that walks q upward waits only for the vectors it needs.
+template <bool BF16, int VEC, int Q0, int Q1>
+__device__ __forceinline__ void load_full_range(const KArgs& a, int row, uint32_t c0,
+                                                float (&x)[VEC][Elem<BF16>::EPV]) {
     typedef typename Elem<BF16>::T T;
     const T* base = (const T*)a.logits + (int64_t)row * a.row_stride + c0 + (uint32_t)threadIdx.x * Elem<BF16>::EPV;
     uint4 w[VEC];
 #pragma unroll
-    for (int q = 0; q < VEC; q++) {
+    for (int q = Q0; q < Q1; q++) {
         w[q] = *(const uint4*)(base + (uint32_t)(q * BLOCK) * Elem<BF16>::EPV);
         __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int q = 0; q < VEC; q++) unpack16<BF16, VEC>(w[q], x[q]);
+    for (int q = Q0; q < Q1; q++) unpack16<BF16, VEC>(w[q], x[q]);
+}
+template <bool BF16, int VEC>
+__device__ __forceinline__ void load_full_tile(const KArgs& a, int row, uint32_t c0,
+                                               float (&x)[VEC][Elem<BF16>::EPV]) {
+    load_full_range<BF16, VEC, 0, VEC>(a, row, c0, x);
 }
 
 template <bool BF16, int VEC>

@@ -1376,7 +1376,10 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
     const uint64_t V = (uint64_t)a.V;
 
     uint64_t n_finite;
+    BFI_TRACE(a, 0, 4);
     const uint64_t S_fix = vsel_l1<BF16, VEC>(a, sm, C, P, M, scale, &n_finite);
+    BFI_TRACE(a, 0, 5);
+    int nq = 0;
     const uint64_t Lk = C.kmode ? (uint64_t)C.k : V;
     uint64_t Lp = ~0ull, Lm = ~0ull, L = 0, T = 0, kept_mass = 0, kd = ~0ull, md = 0;
     Sel selp{0, 0, 0}, last{0, 0, 0};
@@ -1492,6 +1495,8 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
             exm = md;
         }
         const Sel r = vsel_query<BF16, VEC>(a, sm, C, P, M, scale, kind, target, ex, exm);
+        if (nq < 3) BFI_TRACE(a, 0, 12 + nq);
+        nq++;
         if (st == Q_K) {  // top-p runs over the top-k list: cut inside it, or keep all k
             if (r.cum_mass < T) {
                 Lp = Lk;

@@ -131,23 +131,11 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
     // The loads depend on kernel arguments only and go out first: the row's parameters
     // (scalar loads that queue behind other workgroups' traffic) arrive meanwhile. The
     // allow-mask words go before the logits, so pass 1 can start on the first vector while
-    // the rest are in flight.
-    // A history of at most PREPEN_H ids is applied here (sample.rs:345-367): its ids are
-    // loaded first, so they land before this workgroup's logits (two scalar loads of the
-    // row's offsets precede them).
-    constexpr int HPT = PREPEN_H / BLOCK;
-    uint32_t hid[HPT];
-    {
-        const HistView hv = row_history(a, row);
-        const int64_t hn = hv.size();
-        if (hn > 0 && hn <= (int64_t)PREPEN_H) {
-#pragma unroll
-            for (int g = 0; g < HPT; g++) {
-                const int64_t j = (int64_t)g * BLOCK + tid;
-                hid[g] = j < hn ? hv.at(j) : 0xFFFFFFFFu;
-            }
-        }
-    }
+    // the rest are in flight. A history of at most PREPEN_H ids is applied here
+    // (sample.rs:345-367): its ids go out after the first half of a full chunk's logits, so
+    // that the two scalar loads of the row's offsets they need do not hold up the logits,
+    // and before the second half, so they land while pass 1 is still waiting for data.
+    const HistView hv = row_history(a, row);
     const uint32_t* mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
     uint32_t mwd[VEC];
     if (mrow) {
@@ -158,15 +146,28 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
         }
     }
     float x[VEC][EPV];
-    if (FULL) load_full_tile<BF16, VEC>(a, row, c0, x);
+    if (FULL) load_full_range<BF16, VEC, 0, (VEC + 1) / 2>(a, row, c0, x);
+    constexpr int HPT = PREPEN_H / BLOCK;
+    uint32_t hid[HPT];
+    {
+        const int64_t hn = hv.size();
+        if (hn > 0 && hn <= (int64_t)PREPEN_H) {
+#pragma unroll
+            for (int g = 0; g < HPT; g++) {
+                const int64_t j = (int64_t)g * BLOCK + tid;
+                hid[g] = j < hn ? hv.at(j) : 0xFFFFFFFFu;
+            }
+        }
+    }
+    if (FULL) load_full_range<BF16, VEC, (VEC + 1) / 2, VEC>(a, row, c0, x);
     else load_tile<BF16, VEC>(a, row, c0, c1, x);
     BFI_STAMP(1);
     const RowCtx C = make_ctx(a, row);
     if (!C.active) return;  // a verify row past its draft: the loads are dropped
 
-    // penalties: the ids inside this chunk are counted in LDS (the ids land before the
-    // logits; the barriers pass while the logits are in flight), then each thread reads the
-    // counts of its elements and pass 1 penalizes them as they arrive
+    // penalties: the ids inside this chunk are counted in LDS (the barriers pass while the
+    // second half of the logits is in flight), then each thread reads the counts of its
+    // elements and pass 1 penalizes them as they arrive
     uint32_t cw[VEC][EPV / 2];
     if (C.prepen) {
         uint4* hc4 = reinterpret_cast<uint4*>(sm.u.hc);
