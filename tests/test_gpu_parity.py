@@ -401,3 +401,82 @@ def test_c1_full_size_and_topk_over_many_chunks(smp):
         cfg = _cfg_from([rows[i]], [params[i]], [hist[i]], u=[0.3 + 0.2 * i])
         cfg["name"] = f"topk-many-chunks-{i}"
         check(cfg, 2048, smp)
+
+
+def test_verify_with_penalties(smp):
+    """Spec verify with histories and penalties: row i of a sequence also counts the drafts
+    before it (spec.rs:137-162 appends each accepted draft), both for histories the stream
+    pass applies and for longer ones the select pass corrects. Top-k bounds the kept sets:
+    a top-p set of thousands of ids ends where the reference's sequential f32 sums (whose
+    error reaches 1e-4 at this size) and exact ones can disagree, which verify's residual draw
+    then shows (the sampling tests exempt that band; verify has no such exemption)."""
+    import torch
+
+    rng = np.random.default_rng(16)
+    cfg = workloads.config("C4", seed=1, scale_v=0.25)
+    S, R, V = cfg["n_seq"], cfg["rows_per_seq"], cfg["V"]
+    hists = []
+    for s in range(S):
+        n = [0, 40, 700, 1500][s % 4]
+        h = rng.integers(0, V, n).astype(np.uint32)
+        if n:
+            h[: min(n, 8)] = cfg["drafts"][s, 0]  # the first draft repeated: counts > 1
+        hists.append(h)
+    cfg["hist"] = np.concatenate(hists).astype(np.uint32) if any(len(h) for h in hists) else np.zeros(0, np.uint32)
+    cfg["hist_off"] = np.cumsum([0] + [len(h) for h in hists]).astype(np.int64)
+    params = cfg["params"].copy()
+    for s in range(S):
+        params[s]["repeat_penalty"] = [1.0, 1.3, 0.8, 1.1][s % 4]
+        params[s]["presence_penalty"] = [0.0, 0.4, -0.2, 0.5][(s // 4) % 4]
+        params[s]["frequency_penalty"] = [0.0, 0.2][s % 2]
+        params[s]["top_k"] = [40, 100, 20, 60][(s // 2) % 4]
+        params[s]["min_p"] = [0.0, 0.05][(s // 8) % 2]
+    cfg["params"] = params
+    d = workloads.to_device(cfg)
+    smp.verify(d["logits"], R, d["params"], d["drafts"], d["draft_len"], d["u_pairs"], d["u_bonus"],
+               d["out_accepted"], d["out_next"], d["hist"], d["hist_off"], d["mask"])
+    torch.cuda.synchronize()
+    acc = d["out_accepted"].cpu().numpy()
+    nxt = d["out_next"].cpu().numpy().astype(np.uint32)
+    ref = oracle_verify(cfg)
+    bad = []
+    for s, (a_o, n_o) in enumerate(ref):
+        if (acc[s], nxt[s]) == (a_o, n_o):
+            continue
+        ok = False
+        for dv in np.linspace(-1e-6, 1e-6, 5):
+            up = (cfg["u_pairs"] + np.float32(dv)).astype(np.float32)
+            ub = (cfg["u_bonus"] + np.float32(dv)).astype(np.float32)
+            if oracle_verify(cfg, up, ub)[s] == (acc[s], nxt[s]):
+                ok = True
+                break
+        if not ok:
+            bad.append((s, int(acc[s]), int(nxt[s]), a_o, n_o))
+    print(f"[parity] verify+penalties accepted={acc.tolist()}", flush=True)
+    assert not bad, bad
+
+
+def test_penalized_rows_across_chunks(smp):
+    """Penalties over many chunks: greedy rows (argmax of the penalized logits), rows with
+    min_p > 1 (fallback to the masked, un-penalized argmax, which a penalty may have moved),
+    top-k / top-p / min-p rows; histories just below and above the stream pass's limit, with
+    duplicates, ids >= V and the row maximum in them."""
+    rng = np.random.default_rng(17)
+    V = 60000
+    rows, params, hist = [], [], []
+    modes = [dict(temperature=0.0), dict(temperature=0.9, min_p=2.0), dict(temperature=0.9, top_k=30),
+             dict(temperature=1.1, top_p=0.9, min_p=0.02), dict(temperature=0.6, min_p=0.1)]
+    for m in modes:
+        for n in (1024, 1025, 300):
+            x = (rng.standard_normal(V) * 2.0).astype(np.float32)
+            x[rng.choice(V, 6, replace=False)] += 8.0
+            h = rng.integers(0, V, n).astype(np.uint32)
+            h[:5] = np.argmax(x)  # the row maximum, five times
+            h[5] = V + 7  # outside the vocabulary: ignored
+            rows.append(x)
+            hist.append(h.tolist())
+            params.append({**m, "repeat_penalty": 1.4, "presence_penalty": 0.3, "frequency_penalty": 0.25})
+    u = rng.random(len(rows)).astype(np.float32)
+    cfg = _cfg_from(rows, params, hist, u=u.tolist())
+    cfg["name"] = "penalized-rows"
+    check(cfg, 512, smp)
