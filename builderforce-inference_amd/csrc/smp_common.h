@@ -292,8 +292,11 @@ __device__ __forceinline__ uint32_t tile_count_ge(const float (&x)[VEC][Elem<BF1
     return c;
 }
 
+// The fixed-point mass of value s in a row with maximum M (the radix select's unit: its cuts
+// and draws compare sums of these integers, so only their consistency matters, not the
+// last ulp of the exponential; the hardware exp2 keeps the row passes short).
 __device__ __forceinline__ uint64_t efix_of(float s, float M, double scale) {
-    float e = expf(s - M);
+    const float e = __builtin_amdgcn_exp2f((s - M) * 1.44269504088896341f);
     return (uint64_t)((double)e * scale);
 }
 
