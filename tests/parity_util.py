@@ -4,7 +4,8 @@ Token ids must equal the oracle's. The only exemption is a draw whose u lies wit
 of a CDF boundary, and it is checked constructively: the oracle, re-run with some
 u' in [u - 1e-6, u + 1e-6], must return the GPU's token. Kept sets must be equal, except at
 a top-p boundary, where the exact (float64) cumulative mass at the cut is within BAND of
-top_p. In that case the reference's own float32 sequential sum decides the cut. Probabilities
+top_p, widened to the reference's own float32 normalizer error on that row. In that case
+the reference's float32 sequential sum decides the cut. Probabilities
 must agree within 1e-5 relative, or within 2e-6 relative of the float64 value when the
 reference's sequential float32 normalizer is itself off by more than that.
 """
@@ -30,15 +31,25 @@ def exact_probs(s):
     return e / e.sum()
 
 
-def top_p_band(s, top_p, lens):
-    """True when the float64 cumulative mass near the cut is within BAND of top_p."""
+def top_p_band(s, top_p, lens, ref_sum=None):
+    """True when the float64 cumulative mass near the cut is within the band of top_p: BAND,
+    widened to what the reference's own float32 arithmetic demonstrably gets wrong on this
+    row when its sequential normalizer `ref_sum` is given (twice the normalizer's relative
+    error, which sequential summation of 10^4+ terms pushes past 1e-5 by dropping small
+    terms, plus one rounding per cumsum step)."""
     pr = exact_probs(s)
     if pr is None:
         return False
     order = np.argsort(-pr, kind="stable")
     cum = np.cumsum(pr[order])
     lo, hi = max(min(lens) - 2, 0), min(max(lens), len(cum))
-    return bool(np.any(np.abs(cum[lo:hi] - top_p) <= BAND))
+    band = BAND
+    if ref_sum is not None:
+        sv = s.astype(np.float64)
+        fin = np.isfinite(sv)
+        s_exact = float(np.sum(np.exp(sv[fin] - np.max(sv[fin]))))
+        band = max(BAND, 2.0 * abs(float(ref_sum) / s_exact - 1.0) + hi * 6e-8)
+    return bool(np.any(np.abs(cum[lo:hi] - top_p) <= band))
 
 
 def band_draw(s, kept_len, u):
@@ -86,7 +97,9 @@ def compare_target(cfg, gpu, orc, logits_f32=None, check_list=True):
         kl_o, kl_g = int(orc["kept_len"][b]), int(gpu["kept_len"][b])
         band = False
         if kl_o != kl_g:
-            if p["top_p"] < 1.0 and orc.get("s") is not None and top_p_band(orc["s"][b], p["top_p"], (kl_o, kl_g)):
+            ref_sum = orc["stats"][b, 1] if "stats" in orc else None
+            if p["top_p"] < 1.0 and orc.get("s") is not None and \
+                    top_p_band(orc["s"][b], p["top_p"], (kl_o, kl_g), ref_sum):
                 band = True
                 stats["band_exempt"] += 1
             else:

@@ -111,6 +111,7 @@ def test_host_path_matches_oracle_on_random_small_rows(smp):
         ("C3", 0.05, False, 0),
         ("C3", 0.05, True, 0),
         ("C5", 0.01, False, 0),
+        ("C5", 0.1, False, 1),
     ],
 )
 def test_config_parity_reduced(smp, name, scale, greedy, seed):
