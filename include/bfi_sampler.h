@@ -90,7 +90,8 @@ int bfi_smp_profile(bfi_smp_ctx *ctx, double *stream_ms, double *select_ms, int6
 
 /* Phase trace (diagnostics, no counterpart in the reference): while enabled, each launch
  * records wall-clock (100 MHz) timestamps at phase boundaries of every workgroup into a
- * context buffer: 8 words per streaming workgroup, then 8 per selection workgroup.
+ * context buffer: 8 words per streaming workgroup (row-major by row, chunk), then 16 per
+ * row for its selection workgroup.
  * bfi_smp_trace copies the last launch's record (synchronous) and returns the word count. */
 int bfi_smp_set_tracing(bfi_smp_ctx *ctx, int enabled);
 int64_t bfi_smp_trace(bfi_smp_ctx *ctx, uint64_t *out, int64_t max_words);
