@@ -295,9 +295,15 @@ __device__ __forceinline__ uint32_t tile_count_ge(const float (&x)[VEC][Elem<BF1
 // The fixed-point mass of value s in a row with maximum M (the radix select's unit: its cuts
 // and draws compare sums of these integers, so only their consistency matters, not the
 // last ulp of the exponential; the hardware exp2 keeps the row passes short).
+// It equals floor(e * scale) for scale = 2^b, 32 <= b <= 62, in f32 arithmetic: t = e * 2^(b-32)
+// is exact (a power-of-two scaling of e <= 1), floor(t) < 2^31 is the high word, and the
+// fraction t - floor(t) (exact for t >= 0) times 2^32, truncated, is the low word.
 __device__ __forceinline__ uint64_t efix_of(float s, float M, double scale) {
     const float e = __builtin_amdgcn_exp2f((s - M) * 1.44269504088896341f);
-    return (uint64_t)((double)e * scale);
+    const float t = e * (float)(scale * 0x1p-32);
+    const uint32_t hi = (uint32_t)t;
+    const uint32_t lo = (uint32_t)(__builtin_amdgcn_fractf(t) * 0x1p32f);
+    return ((uint64_t)hi << 32) | lo;
 }
 
 }  // namespace bfi

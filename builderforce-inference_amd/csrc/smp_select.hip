@@ -343,11 +343,109 @@ __device__ __forceinline__ uint32_t pen_count(const Smem& sm, const PenSrc& S, c
     return S.gcnt[dense_rank(S.gpre[id >> 5], S.gbm[id >> 5], id & 31)];
 }
 
-// In place over one tile of a pass over the row: the streaming value (raw_value) for every
-// element, the penalized value (pen_value) for the history ids.
+// Raw words of one tile of a pass over the row: 16 bytes of logits, the allow-mask word and
+// the history-membership word of every vector the thread owns. A tile's words are loaded as
+// one batch before the previous tile is processed, and nothing reads them until then, so the
+// loads of the next tile stay in flight while this one is worked on.
 template <bool BF16, int VEC>
-__device__ __forceinline__ void transform_tile(const Smem& sm, const RowCtx& C, const PenSrc& S, uint32_t c0,
-                                               uint32_t c1, float (&x)[VEC][Elem<BF16>::EPV]) {
+struct RawTile {
+    uint4 w[VEC];
+    uint32_t mw[VEC];
+    uint32_t pw[VEC];
+};
+
+template <bool BF16, int VEC>
+__device__ __forceinline__ void load_raw(const KArgs& a, const RowCtx& C, const PenSrc& P, uint32_t c0,
+                                         uint32_t c1, RawTile<BF16, VEC>& r) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    typedef typename Elem<BF16>::T T;
+    const T* base = (const T*)a.logits + (int64_t)C.row * a.row_stride;
+    const int tid = threadIdx.x;
+    const uint32_t ninf = BF16 ? 0xFF80FF80u : 0xFF800000u;  // -inf in every element
+    if (a.vec_ok && c1 - c0 == (uint32_t)(BLOCK * VEC * EPV)) {
+#pragma unroll
+        for (int q = 0; q < VEC; q++) r.w[q] = *(const uint4*)(base + c0 + (uint32_t)(q * BLOCK + tid) * EPV);
+    } else {
+#pragma unroll
+        for (int q = 0; q < VEC; q++) {
+            const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
+            if (a.vec_ok && id0 + EPV <= c1) {
+                r.w[q] = *(const uint4*)(base + id0);
+            } else {
+                uint32_t ww[4] = {ninf, ninf, ninf, ninf};
+#pragma unroll
+                for (int e = 0; e < EPV; e++) {
+                    if (id0 + e >= c1) continue;
+                    if (BF16) {
+                        const uint32_t b = (uint32_t)base[id0 + e];
+                        ww[e >> 1] = (e & 1) ? (ww[e >> 1] & 0xFFFFu) | (b << 16) : (ww[e >> 1] & 0xFFFF0000u) | b;
+                    } else {
+                        ww[e] = __float_as_uint((float)base[id0 + e]);
+                    }
+                }
+                r.w[q] = make_uint4(ww[0], ww[1], ww[2], ww[3]);
+            }
+        }
+    }
+    // Every path issues the same loads: word indices clamped into the row, and a table the
+    // row does not have read from the row's own logits (wi < V/32 words lie inside them) and
+    // replaced afterwards. The compiler's waits before this tile's first use then count the
+    // loads issued after it on every path alike.
+    const bool pen_tab = C.pen_on && !P.hash;
+    const uint32_t* mp = C.mrow ? C.mrow : (const uint32_t*)base;
+    const uint32_t* pp = pen_tab ? P.gbm : (const uint32_t*)base;
+#pragma unroll
+    for (int q = 0; q < VEC; q++) {
+        const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
+        const uint32_t wi = id0 < c1 ? id0 >> 5 : 0u;
+        r.mw[q] = mp[wi];
+        r.pw[q] = pp[wi];
+    }
+}
+
+// Streaming values (raw_value) of one vector without penalties: one range check for the
+// vector, then the division of div_T_fast without its per-element branches (no element is
+// infinite or NaN there); other vectors take raw_value per element.
+template <int EPV>
+__device__ __forceinline__ void raw_vector(const RowCtx& C, float (&x)[EPV], uint32_t mb) {
+    if (C.greedy) {
+#pragma unroll
+        for (int e = 0; e < EPV; e++) x[e] = ((mb >> e) & 1u) ? x[e] : -__builtin_inff();
+        return;
+    }
+    if (C.fast_div) {
+        uint32_t hi = 0u, lo = 0xFFFFFFFFu;
+#pragma unroll
+        for (int e = 0; e < EPV; e++) {
+            const uint32_t ab = __float_as_uint(x[e]) & 0x7FFFFFFFu;
+            hi = max(hi, ab);
+            lo = min(lo, ab - 1u);
+        }
+        // every element zero or with |x| in [2^-100, 2^100): div_ok holds for all of them
+        if (hi < 0x71800000u && lo >= 0x0D7FFFFFu) {
+#pragma unroll
+            for (int e = 0; e < EPV; e++) {
+                const float q = x[e] * C.rT;
+                const float er = __builtin_fmaf(-q, C.T, x[e]);
+                x[e] = __builtin_fmaf(er, C.rT, q);
+            }
+            if (C.mrow) {
+#pragma unroll
+                for (int e = 0; e < EPV; e++) x[e] = ((mb >> e) & 1u) ? x[e] : -__builtin_inff();
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPV; e++) x[e] = raw_value(C, x[e], (mb >> e) & 1u);
+}
+
+// In place over one tile of a pass over the row (words in r): the streaming value
+// (raw_value) for every element, the penalized value (pen_value) for the history ids.
+template <bool BF16, int VEC>
+__device__ __forceinline__ void transform_raw(const Smem& sm, const RowCtx& C, const PenSrc& S, uint32_t c0,
+                                              uint32_t c1, const RawTile<BF16, VEC>& r,
+                                              float (&x)[VEC][Elem<BF16>::EPV]) {
     constexpr int EPV = Elem<BF16>::EPV;
     const int tid = threadIdx.x;
     const uint32_t em = (1u << EPV) - 1u;
@@ -355,16 +453,15 @@ __device__ __forceinline__ void transform_tile(const Smem& sm, const RowCtx& C, 
     for (int q = 0; q < VEC; q++) {
         const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
         if (id0 >= c1) continue;  // all -inf already
-        const uint32_t mb = C.mrow ? (C.mrow[id0 >> 5] >> (id0 & 31)) & em : em;
-        const uint32_t pb = C.pen_on ? pen_bits(sm, S, id0, EPV) : 0u;
+        const uint32_t mb = C.mrow ? (r.mw[q] >> (id0 & 31)) & em : em;
+        const uint32_t pb = !C.pen_on ? 0u : S.hash ? pen_bits(sm, S, id0, EPV) : (r.pw[q] >> (id0 & 31)) & em;
         if (pb) {  // rare: an id of the history in this vector
 #pragma unroll
             for (int e = 0; e < EPV; e++)
                 x[q][e] = ((pb >> e) & 1u) ? pen_value(C, x[q][e], (mb >> e) & 1u, pen_count(sm, S, C, id0 + e))
                                            : raw_value(C, x[q][e], (mb >> e) & 1u);
         } else {
-#pragma unroll
-            for (int e = 0; e < EPV; e++) x[q][e] = raw_value(C, x[q][e], (mb >> e) & 1u);
+            raw_vector<EPV>(C, x[q], mb);
         }
     }
 }
@@ -378,19 +475,19 @@ __device__ __forceinline__ void span_pass(const KArgs& a, const Smem& sm, const 
     constexpr int EPV = Elem<BF16>::EPV;
     constexpr uint32_t TILE = (uint32_t)BLOCK * VEC * EPV;
     const uint32_t em = (1u << EPV) - 1u;
-    // the next tile's loads are issued before this tile is processed
-    float x[VEC][EPV], xn[VEC][EPV];
-    if (c0 < c1) load_tile<BF16, VEC>(a, C.row, c0, min(c0 + TILE, c1), x);
-    for (uint32_t t0 = c0; t0 < c1; t0 += TILE) {
-        const uint32_t t1 = min(t0 + TILE, c1);
-        if (t1 < c1) load_tile<BF16, VEC>(a, C.row, t1, min(t1 + TILE, c1), xn);
-        if (!SKIP_HIST) transform_tile<BF16, VEC>(sm, C, P, t0, t1, x);
+    // two buffers, the loop unrolled by two: a tile's words are consumed from the registers
+    // they were loaded into (a copy between buffers would wait for the loads in flight)
+    RawTile<BF16, VEC> ra, rb;
+    auto tile = [&](const RawTile<BF16, VEC>& r, uint32_t t0, uint32_t t1) __attribute__((always_inline)) {
+        float x[VEC][EPV];
+#pragma unroll
+        for (int q = 0; q < VEC; q++) unpack16<BF16, VEC>(r.w[q], x[q]);
+        if (!SKIP_HIST) transform_raw<BF16, VEC>(sm, C, P, t0, t1, r, x);
 #pragma unroll
         for (int q = 0; q < VEC; q++) {
             const uint32_t id0 = t0 + (uint32_t)(q * BLOCK + threadIdx.x) * EPV;
             if (id0 >= t1) continue;
-            uint32_t mb = em;
-            if (SKIP_HIST && C.mrow) mb = (C.mrow[id0 >> 5] >> (id0 & 31)) & em;
+            const uint32_t mb = (SKIP_HIST && C.mrow) ? (r.mw[q] >> (id0 & 31)) & em : em;
 #pragma unroll
             for (int e = 0; e < EPV; e++) {
                 const uint32_t id = id0 + e;
@@ -403,10 +500,22 @@ __device__ __forceinline__ void span_pass(const KArgs& a, const Smem& sm, const 
                 }
             }
         }
-#pragma unroll
-        for (int q = 0; q < VEC; q++)
-#pragma unroll
-            for (int e = 0; e < EPV; e++) x[q][e] = xn[q][e];
+    };
+    // past the span's last tile, the "next" loads re-read the tile just loaded (cached), so
+    // that every iteration issues the same loads
+    if (c0 >= c1) return;
+    load_raw<BF16, VEC>(a, C, P, c0, min(c0 + TILE, c1), ra);
+    for (uint32_t t0 = c0;; t0 += 2 * TILE) {
+        const uint32_t t1 = min(t0 + TILE, c1);
+        const bool more1 = t1 < c1;
+        load_raw<BF16, VEC>(a, C, P, more1 ? t1 : t0, more1 ? min(t1 + TILE, c1) : t1, rb);
+        tile(ra, t0, t1);
+        if (!more1) break;
+        const uint32_t t2 = min(t1 + TILE, c1);
+        const bool more2 = t2 < c1;
+        load_raw<BF16, VEC>(a, C, P, more2 ? t2 : t1, more2 ? min(t2 + TILE, c1) : t2, ra);
+        tile(rb, t1, t2);
+        if (!more2) break;
     }
 }
 
@@ -836,8 +945,11 @@ __device__ __forceinline__ void tile_weights(const KArgs& a, const Smem& sm, con
                                              uint32_t t0, uint32_t t1, float M, float S, float thresh, uint32_t excl,
                                              float (&x)[VEC][Elem<BF16>::EPV]) {
     constexpr int EPV = Elem<BF16>::EPV;
-    load_tile<BF16, VEC>(a, C.row, t0, t1, x);
-    transform_tile<BF16, VEC>(sm, C, P, t0, t1, x);
+    RawTile<BF16, VEC> r;
+    load_raw<BF16, VEC>(a, C, P, t0, t1, r);
+#pragma unroll
+    for (int q = 0; q < VEC; q++) unpack16<BF16, VEC>(r.w[q], x[q]);
+    transform_raw<BF16, VEC>(sm, C, P, t0, t1, r, x);
 #pragma unroll
     for (int q = 0; q < VEC; q++)
 #pragma unroll
