@@ -32,6 +32,8 @@ namespace bfi {
 
 // ---- shared memory ---------------------------------------------------------------------
 
+constexpr int NSPEC = 512;  // elements of the buckets gathered ahead for a following query
+
 struct __align__(16) Smem {
     union {
         struct {
@@ -66,6 +68,10 @@ struct __align__(16) Smem {
     uint64_t r64[NWAVE];
     uint64_t r64b[NWAVE];
     uint32_t misc[8];
+    // value buckets spec_lo..spec_hi of the row, complete (every element), gathered with an
+    // earlier query for a query expected to follow; spec_lo > spec_hi when empty
+    uint64_t spec[NSPEC];
+    uint32_t spec_n, spec_lo, spec_hi;
     uint32_t fx[8];   // the fast finish's row values
     uint64_t tr[16];  // phase timestamps of this workgroup (diagnostics)
     // row aggregates built with LDS atomics (integer, so independent of the order)
@@ -1360,10 +1366,25 @@ __device__ __forceinline__ uint64_t vsel_l1(const KArgs& a, Smem& sm, const RowC
     return tot;
 }
 
-// radix_select's query by value buckets (vsel_l1 must have run for this row).
+// The query expected after a top-p cut, whose buckets the cut's gather collects ahead:
+// mode 1, the draw at ceil(u * kept); mode 2, the residual draw of a verify row at
+// ceil(u * (kept - md)) without the draft (bucket bd, mass md) when the draft is kept, at
+// ceil(u * kept) when it is not.
+struct SpecReq {
+    int mode;
+    double u;
+    uint64_t md;
+    uint32_t bd;
+};
+
+// radix_select's query by value buckets (vsel_l1 must have run for this row). With `sr`, the
+// gather also collects the buckets the following query can need (the kept mass lies between
+// the cut bucket's exclusive and inclusive cumulative masses); a query whose bucket lies in
+// the collected range takes it from LDS instead of a pass over the row.
 template <bool BF16, int VEC>
 __device__ __forceinline__ Sel vsel_query(const KArgs& a, Smem& sm, const RowCtx& C, const PenSrc& P, float M,
-                                          double scale, int kind, uint64_t target, uint64_t excl, uint64_t excl_mass) {
+                                          double scale, int kind, uint64_t target, uint64_t excl, uint64_t excl_mass,
+                                          SpecReq sr = SpecReq{0, 0.0, 0, 0}) {
     constexpr int BPT = NVB / BLOCK;
     const int tid = threadIdx.x;
     const uint64_t* saved = a.row_hist + (int64_t)C.row * NVB * 2;
@@ -1419,23 +1440,108 @@ __device__ __forceinline__ Sel vsel_query(const KArgs& a, Smem& sm, const RowCtx
         sm.r64[0] = cab;
         sm.r64b[0] = mab;
         sm.r64[1] = nbk;
+        sm.r64b[1] = pm + lm[i];  // inclusive cumulative mass through the bucket
     }
     __syncthreads();
-    const uint64_t before_cnt = sm.r64[0], before_mass = sm.r64b[0], nbk = sm.r64[1];
+    const uint64_t before_cnt = sm.r64[0], before_mass = sm.r64b[0], nbk = sm.r64[1], incl_mass = sm.r64b[1];
+    const bool cached = sm.spec_lo <= hit && hit <= sm.spec_hi;
     __syncthreads();
     if (nbk > (uint64_t)NMAX || nbk == 0)  // too dense to sort in LDS
         return radix_select<BF16, VEC>(a, sm, C, P, M, scale, kind, target, excl, excl_mass);
-    // gather the bucket, sort it, walk it
-    if (tid == 0) sm.misc[MISC_N] = 0;
+    // the bucket of mass target t (as `hit` above) when element mass xm in bucket xb is
+    // left out
+    auto mass_bucket = [&](uint64_t t, uint32_t xb2, uint64_t xm2) __attribute__((always_inline)) {
+        uint32_t h = 0xFFFFFFFFu, l = 0;
+#pragma unroll
+        for (int i = 0; i < BPT; i++) {
+            const uint32_t b = (uint32_t)tid * BPT + i;
+            const uint64_t c = bc[i] - (b == xb2 ? 1u : 0u);
+            const uint64_t cm = pm + lm[i] - (b >= xb2 ? xm2 : 0ull);
+            if (h == 0xFFFFFFFFu && c > 0 && cm >= t) h = b;
+            if (c > 0) l = b + 1;
+        }
+        h = block_min_u(h, sm.ru);
+        if (h == 0xFFFFFFFFu) {
+            l = (uint32_t)block_max_u64(l, sm.r64);
+            h = l ? l - 1 : 0;
+        }
+        return h;
+    };
+    // inclusive cumulative count through bucket b
+    auto cum_cnt = [&](uint32_t b) __attribute__((always_inline)) {
+        if ((uint32_t)tid == b / BPT) {
+            uint64_t v = 0;
+#pragma unroll
+            for (int ii = 0; ii < BPT; ii++)
+                if ((uint32_t)ii == b % BPT) v = pc + lc[ii];
+            sm.r64[2] = v;
+        }
+        __syncthreads();
+        const uint64_t v = sm.r64[2];
+        __syncthreads();
+        return v;
+    };
+    uint32_t slo = 1u, shi = 0u;
+    if (sr.mode && !cached && excl == ~0ull) {
+        const bool can_drop = sr.mode == 1 || sr.bd >= hit;  // the draft may be outside the kept set
+        const bool can_keep = sr.mode == 2 && sr.bd <= hit;
+        slo = 0xFFFFFFFFu;
+        shi = 0u;
+        if (can_drop) {  // ceil(u * kept), kept in [before, incl]
+            slo = min(slo, mass_bucket((uint64_t)ceil(sr.u * (double)before_mass), 0xFFFFFFFFu, 0ull));
+            shi = max(shi, mass_bucket((uint64_t)ceil(sr.u * (double)incl_mass), 0xFFFFFFFFu, 0ull));
+        }
+        if (can_keep) {  // ceil(u * (kept - md)) without the draft, kept - md in [lo, incl - md]
+            const uint64_t lo = sr.bd < hit ? before_mass - sr.md : before_mass;
+            slo = min(slo, mass_bucket((uint64_t)ceil(sr.u * (double)lo), sr.bd, sr.md));
+            shi = max(shi, mass_bucket((uint64_t)ceil(sr.u * (double)(incl_mass - sr.md)), sr.bd, sr.md));
+        }
+        if (slo <= shi) {  // only a range that fits
+            const uint64_t n_in = cum_cnt(shi) - (slo ? cum_cnt(slo - 1) : 0ull);
+            if (n_in > (uint64_t)NSPEC) {
+                slo = 1u;
+                shi = 0u;
+            }
+        }
+    }
+    const bool spec_on = slo <= shi;
+    // the bucket (without `excl`) into the list: from the buckets gathered ahead, or a pass
+    if (tid == 0) {
+        sm.misc[MISC_N] = 0;
+        if (spec_on) sm.spec_n = 0;
+    }
     __syncthreads();
-    row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) __attribute__((always_inline)) {
-        if (!(s > -__builtin_inff()) || vbucket(s, M) != hit) return;
-        const uint64_t k = key64(s, id);
-        if (k == excl) return;
-        const uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
-        if (slot < NMAX) sm.u.cb.keys[slot] = k;
-    });
+    if (cached) {
+        const int ns = (int)sm.spec_n;
+        for (int j = tid; j < ns; j += BLOCK) {
+            const uint64_t k = sm.spec[j];
+            if (vbucket(key_s(k), M) != hit || k == excl) continue;
+            const uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+            if (slot < NMAX) sm.u.cb.keys[slot] = k;
+        }
+    } else {
+        row_pass<BF16, VEC>(a, sm, C, P, [&](uint32_t id, float s) __attribute__((always_inline)) {
+            if (!(s > -__builtin_inff())) return;
+            const uint32_t b = vbucket(s, M);
+            const bool in_spec = spec_on && b - slo <= shi - slo;
+            if (b != hit && !in_spec) return;
+            const uint64_t k = key64(s, id);
+            if (b == hit && k != excl) {
+                const uint32_t slot = lds_add(&sm.misc[MISC_N], 1u);
+                if (slot < NMAX) sm.u.cb.keys[slot] = k;
+            }
+            if (in_spec) {
+                const uint32_t slot = lds_add(&sm.spec_n, 1u);
+                if (slot < NSPEC) sm.spec[slot] = k;
+            }
+        });
+    }
     __syncthreads();
+    if (spec_on && tid == 0) {  // complete, or unusable
+        const bool fits = sm.spec_n <= (uint32_t)NSPEC;
+        sm.spec_lo = fits ? slo : 1u;
+        sm.spec_hi = fits ? shi : 0u;
+    }
     const int N = (int)min(sm.misc[MISC_N], (uint32_t)NMAX);
     if (N <= BLOCK && N > WAVE) sort_list_regs(sm, N);
     else sort_list(sm, N);
@@ -1489,6 +1595,13 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
 
     uint64_t n_finite;
     BFI_TRACE(a, 0, 4);
+    if (tid == 0) {
+        sm.spec_lo = 1u;
+        sm.spec_hi = 0u;
+        sm.spec_n = 0u;
+    }
+    // the draft's value, for the judge and the bound of its mass in the residual's buckets
+    const float sd = C.judged ? element_s(a, sm, C, C.draft, BF16, hashed) : -__builtin_inff();
     const uint64_t S_fix = vsel_l1<BF16, VEC>(a, sm, C, P, M, scale, &n_finite);
     BFI_TRACE(a, 0, 5);
     int nq = 0;
@@ -1573,7 +1686,6 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
                 continue;
             }
             // judge (spec.rs:83-95)
-            const float sd = element_s(a, sm, C, C.draft, BF16, hashed);
             const bool kept_d = C.draft < V && key64(sd, C.draft) >= last.key;
             kd = kept_d ? key64(sd, C.draft) : ~0ull;
             md = kept_d ? efix_of(sd, M, scale) : 0ull;
@@ -1606,7 +1718,13 @@ __device__ __forceinline__ void combine_radix(const KArgs& a, Smem& sm, const Ro
             ex = kd;
             exm = md;
         }
-        const Sel r = vsel_query<BF16, VEC>(a, sm, C, P, M, scale, kind, target, ex, exm);
+        SpecReq sr{0, 0.0, 0, 0};
+        if (st == Q_P) {
+            if (!C.judged) sr = SpecReq{1, (double)C.u, 0, 0};
+            else if (sd > -__builtin_inff()) sr = SpecReq{2, (double)C.u2, efix_of(sd, M, scale), vbucket(sd, M)};
+            else sr = SpecReq{2, (double)C.u2, 0, 0xFFFFFFFFu};
+        }
+        const Sel r = vsel_query<BF16, VEC>(a, sm, C, P, M, scale, kind, target, ex, exm, sr);
         if (nq < 3) BFI_TRACE(a, 0, 12 + nq);
         nq++;
         if (st == Q_K) {  // top-p runs over the top-k list: cut inside it, or keep all k
