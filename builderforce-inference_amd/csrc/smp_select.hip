@@ -84,7 +84,7 @@ struct __align__(16) Smem {
         uint32_t thr;     // ord32 of the largest chunk candidate bound
         uint32_t flags;   // 1: some chunk has no candidate list
         uint32_t nd;      // history ids that hold their chunk's maximum
-        uint32_t pad;
+        uint32_t kth;     // ord32 of the k-th largest chunk maximum (top-k rows, k <= chunks)
     } ag;
 };
 
@@ -1861,6 +1861,7 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
         sm.ag.thr = 0u;
         sm.ag.flags = 0u;
         sm.ag.nd = 0u;
+        sm.ag.kth = 0u;
     }
     HistOwn ho;
     const bool hashed = hist_build<BF16>(a, sm, C, ho, [&]() {
@@ -1995,7 +1996,28 @@ __device__ __forceinline__ void select_row(const KArgs& a, Smem& sm) {
             sf += (uint64_t)(wc * FIX44);
         }
         wave_lds_add64(&sm.ag.sfix, sf);
-        const float th_raw = unord_or_ninf(sm.ag.thr);
+        // Top-k rows with k <= chunks: the chunk maxima are k distinct elements at or above the
+        // k-th largest of them (kth), so the row's k-th largest value is too. The reference
+        // orders by p = expf(s - M) / S with ties in index order (sample.rs:392-395), so an
+        // element just below kth can tie in p with one above it: the bound is lowered by the
+        // streaming pass's margin (1e-4 + 1e-5 |s|, far above an ulp of s - M while
+        // s - M > -64), and not used at all further below M, where p nears underflow and
+        // ties at zero. It raises the list bound when the chunk bounds are loose (short
+        // chunks: one row over many chunks).
+        if (C.kmode && (uint32_t)C.k <= (uint32_t)nc) {
+            if (tid < nc && mine.m > -__builtin_inff()) {
+                uint32_t rank = 0;
+                for (int c = 0; c < nc; c++) {
+                    const float o = sm.cm[c];
+                    rank += (o > mine.m || (o == mine.m && c < tid)) ? 1u : 0u;
+                }
+                if (rank == (uint32_t)C.k - 1u) sm.ag.kth = ord32(mine.m);
+            }
+            __syncthreads();
+        }
+        const float kth = unord_or_ninf(sm.ag.kth);
+        const float th_k = kth > M - 64.0f ? kth - (1e-4f + 1e-5f * fabsf(kth)) : -__builtin_inff();
+        const float th_raw = fmaxf(unord_or_ninf(sm.ag.thr), th_k);
         if (bounded) {  // the first pass's list: complete above max(th_raw, min-p bound)
             const float th = fmaxf(th_raw, minp_bound(C, M));
             const bool sorted = C.kmode || C.pmode;
