@@ -404,6 +404,40 @@ def test_c1_full_size_and_topk_over_many_chunks(smp):
         check(cfg, 2048, smp)
 
 
+def test_topk_bound_from_chunk_maxima(smp):
+    """Single rows over 75 chunks with top-k <= chunks, where the k-th largest chunk maximum
+    bounds the list: values on a coarse grid (exact ties in s, and so in p, at the bound,
+    kept in index order), a row whose other values lie more than 64 below the maximum (p
+    underflows: the bound stays off and zero-probability elements fill the top-k in index
+    order), a mask that leaves fewer than k chunks with an allowed element, and a history
+    that penalizes chunk maxima."""
+    rng = np.random.default_rng(21)
+    V = 151936
+    W = (V + 31) // 32
+    grid = (np.round(rng.standard_normal(V) * 10.0) / 4.0).astype(np.float32)
+    far = (rng.standard_normal(V)).astype(np.float32)
+    far[777] = np.float32(150.0)
+    sparse = (rng.standard_normal(V) * 2.5).astype(np.float32)
+    mask = np.zeros(W, np.uint32)
+    for w in rng.choice(W, 6, replace=False):  # at most 6 chunks hold allowed ids
+        mask[w] = np.uint32(0xFFFFFFFF)
+    pen = (rng.standard_normal(V) * 2.5).astype(np.float32)
+    chunk = 2048
+    maxima = [int(c * chunk + np.argmax(pen[c * chunk:(c + 1) * chunk])) for c in range(V // chunk)]
+    cases = [
+        ("grid-k40", grid, dict(temperature=1.0, top_k=40), None, None, 0.61),
+        ("grid-k75-topp", grid, dict(temperature=0.5, top_k=75, top_p=0.9), None, None, 0.13),
+        ("far-k40", far, dict(temperature=1.0, top_k=40), None, None, 0.999),
+        ("far-k8-t03", far, dict(temperature=0.3, top_k=8), None, None, 0.5),
+        ("masked-k20", sparse, dict(temperature=1.0, top_k=20), None, mask, 0.77),
+        ("pen-k30", pen, dict(temperature=0.8, top_k=30, repeat_penalty=1.3), maxima[:40], None, 0.4),
+    ]
+    for name, x, prm, hist, m, u in cases:
+        cfg = _cfg_from([x], [prm], [hist or []], None if m is None else [m], u=[u])
+        cfg["name"] = f"topk-chunk-maxima-{name}"
+        check(cfg, 2048, smp)
+
+
 def test_verify_with_penalties(smp):
     """Spec verify with histories and penalties: row i of a sequence also counts the drafts
     before it (spec.rs:137-162 appends each accepted draft), both for histories the stream
