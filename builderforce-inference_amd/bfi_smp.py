@@ -76,8 +76,34 @@ def lib():
         L.bfi_parse_id_union.restype = I32
         L.bfi_spec_replay.argtypes = [P, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32, I64, ctypes.c_size_t,
                                       ctypes.c_size_t, P, P, P, P, P, P]
+        # allow-mask producer (include/bfi_mask.h)
+        L.bfi_mask_create.argtypes = [I32, ctypes.POINTER(P)]
+        L.bfi_mask_destroy.argtypes = [P]
+        L.bfi_mask_destroy.restype = None
+        L.bfi_mask_error.argtypes = [P]
+        L.bfi_mask_error.restype = ctypes.c_char_p
+        L.bfi_mask_set_vocab.argtypes = [P, P, P, I64]
+        L.bfi_mask_build.argtypes = [P, P, I64, ctypes.POINTER(Constraint), P, ctypes.POINTER(ctypes.c_int32), P]
         _lib = L
     return _lib
+
+
+TOOL_NONE, TOOL_AUTO, TOOL_REQUIRED, TOOL_NAMED = 0, 1, 2, 3
+
+
+class Constraint(ctypes.Structure):
+    """bfi_constraint (include/bfi_mask.h): the constraint fields of SampleParams."""
+    _fields_ = [
+        ("json_object", ctypes.c_int32),
+        ("tool_choice", ctypes.c_int32),
+        ("tool_name", ctypes.c_void_p),
+        ("tool_name_len", ctypes.c_int64),
+        ("tool_names", ctypes.c_void_p),
+        ("tool_name_lens", ctypes.c_void_p),
+        ("n_tool_names", ctypes.c_int32),
+        ("grammar", ctypes.c_void_p),
+        ("grammar_len", ctypes.c_int64),
+    ]
 
 
 def params_array(rows) -> np.ndarray:
@@ -272,3 +298,68 @@ class Sampler:
         """Exactly the reference call: u = Rng(seed).f32() (sample.rs:307)."""
         u, _ = rng_f32(seed)
         return self.sample(logits, prev, params, mask, u)
+
+
+class MaskProducer:
+    """Allow-mask producer of the decode-based constraint (apply_constraint, sample.rs:63-90)
+    over a vocabulary of decoded pieces held on the GPU."""
+
+    def __init__(self, device: int = 0):
+        L = lib()
+        h = ctypes.c_void_p()
+        rc = L.bfi_mask_create(device, ctypes.byref(h))
+        if rc != 0:
+            raise SamplerError(f"bfi_mask_create failed ({rc})")
+        self._h = h
+        self.V = None
+
+    def _check(self, rc):
+        if rc != 0:
+            raise SamplerError(lib().bfi_mask_error(self._h).decode(errors="replace"))
+
+    def set_vocab(self, pieces):
+        """pieces: list of bytes, piece i = decode(i)."""
+        off = np.zeros(len(pieces) + 1, np.int64)
+        off[1:] = np.cumsum([len(x) for x in pieces])
+        blob = np.frombuffer(b"".join(pieces) or b"\0", np.uint8).copy()
+        self._check(lib().bfi_mask_set_vocab(self._h, _np_ptr(blob), _np_ptr(off), len(pieces)))
+        self.V = len(pieces)
+
+    def build(self, so_far: bytes, d_mask, json_object=False, tool_choice=TOOL_NONE, tool_name=b"",
+              tool_names=(), grammar=None, stream=None):
+        """Writes the packed allow-mask into d_mask (torch uint32-compatible int32 tensor of
+        ceil(V/32) words on the GPU); returns 0 when nothing is constrained, else 1."""
+        keep = []
+
+        def buf(b):
+            a = np.frombuffer(b or b"\0", np.uint8).copy()
+            keep.append(a)
+            return _np_ptr(a)
+
+        names = [bytes(n) for n in tool_names]
+        name_ptrs = (ctypes.c_void_p * max(len(names), 1))(*[buf(n) for n in names])
+        name_lens = np.array([len(n) for n in names] or [0], np.int64)
+        g = None if grammar is None else (grammar.encode() if isinstance(grammar, str) else bytes(grammar))
+        c = Constraint(int(bool(json_object)), int(tool_choice), buf(tool_name), len(tool_name),
+                       ctypes.cast(name_ptrs, ctypes.c_void_p), _np_ptr(name_lens), len(names),
+                       None if g is None else buf(g), 0 if g is None else len(g))
+        sf = np.frombuffer(so_far or b"\0", np.uint8).copy()
+        flag = ctypes.c_int32(-1)
+        if stream is None:
+            import torch
+
+            stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        self._check(lib().bfi_mask_build(self._h, _np_ptr(sf), len(so_far), ctypes.byref(c), _dptr(d_mask),
+                                         ctypes.byref(flag), stream))
+        return flag.value
+
+    def close(self):
+        if self._h:
+            lib().bfi_mask_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

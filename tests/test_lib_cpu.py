@@ -1,5 +1,5 @@
 """CPU tests of the C-ABI library: it loads, exports every function include/bfi_sampler.h
-declares, its host-side helpers (Rng, slot_rng, draft, id-union parsing, spec replay) agree
+and include/bfi_mask.h declare, its host-side helpers (Rng, slot_rng, draft, id-union parsing, spec replay) agree
 with the oracle and the reference KATs, and argument errors come back as status codes.
 No GPU work is launched here."""
 import ctypes
@@ -15,12 +15,12 @@ import oracle as O
 import workloads
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "bfi_sampler.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("bfi_sampler.h", "bfi_mask.h")]
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
 def declared_functions():
-    src = open(HEADER).read()
+    src = "".join(open(h).read() for h in HEADERS)
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     return sorted(set(re.findall(r"\b(bfi_[a-z0-9_]+)\s*\(", src)))
 
@@ -28,7 +28,7 @@ def declared_functions():
 def test_library_loads_and_exports_every_declared_symbol():
     L = bfi_smp.lib()
     names = declared_functions()
-    assert len(names) >= 14
+    assert len(names) >= 19
     for n in names:
         assert hasattr(L, n), n
     assert L.bfi_smp_abi_version() == 1
