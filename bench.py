@@ -84,6 +84,63 @@ def cpu_baseline(cfg, seconds):
                        f"{threads} threads")
 
 
+def bench_mask(args):
+    """One step = one bfi_mask_build call (host scan of the generated text + the k_mask
+    launch) for the named tool-call constraint over the synthetic vocabulary; timed with
+    events on the stream. The CPU baseline is the oracle's restatement of apply_constraint
+    (sample.rs:63-90: a rescan of so_far + piece per id) on a sample of ids."""
+    import numpy as np
+    import torch
+
+    import bfi_smp
+    import workloads
+
+    V = 151936
+    pieces = workloads.synthetic_vocab(V, seed=args.seed)
+    mp = bfi_smp.MaskProducer(0)
+    mp.set_vocab(pieces)
+    nw = (V + 31) // 32
+    d = torch.empty(nw, dtype=torch.int32, device="cuda:0")
+    c = workloads.MASK_TOOLS
+    so_far = workloads.MASK_SO_FAR
+    for _ in range(args.warmup):
+        mp.build(so_far, d, **c)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        mp.build(so_far, d, **c)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    piece_bytes = sum(len(p) for p in pieces)
+    moved = piece_bytes + 4 * (V + 1) + 4 * nw
+    line = {"metric": "allow-mask ids/sec (named tool-call constraint, V=151936)", "value": round(V / (ms / 1e3), 1),
+            "unit": "ids/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 5), "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+            "higher_is_better": True, "dtype": "u8", "data": "synthetic vocabulary (workloads.synthetic_vocab)",
+            "config": {"workload": "F1: named tool-call constraint", "n_vocab": V, "so_far_bytes": len(so_far),
+                       "piece_bytes": piece_bytes},
+            "bytes_per_step": moved, "step_gbs": round(moved / (ms / 1e3) / 1e9, 1)}
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import constraint as K
+
+        n, t1 = 0, time.perf_counter()
+        while time.perf_counter() - t1 < args.cpu_seconds and n < V:
+            K.allow_mask(pieces[n:n + 2000], so_far, dict(c))
+            n += 2000
+        dt = time.perf_counter() - t1
+        line["cpu_baseline"] = {"value": round(n / dt, 1), "unit": "ids/s", "cores": 1, "kind": "port",
+                                "sample": f"{n} ids of the same vocabulary through oracle/constraint.py "
+                                          f"(apply_constraint restated: one rescan of so_far + piece per id), "
+                                          f"{dt:.1f} s"}
+    print(json.dumps(line), flush=True)
+    mp.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -96,6 +153,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a device-to-device copy of 256 MiB (10 launches), the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
+    ap.add_argument("--mask", action="store_true",
+                    help="measure the allow-mask producer (include/bfi_mask.h) instead: a named "
+                         "tool-call constraint over a synthetic 151,936-piece vocabulary")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's path runs on a single MI355X "
@@ -117,6 +177,10 @@ def main():
 
     import bfi_smp
     import workloads
+
+    if args.mask:
+        bench_mask(args)
+        return
 
     cfg = workloads.config(args.config, seed=args.seed)
     dev = torch.device("cuda:0")

@@ -329,21 +329,28 @@ class MaskProducer:
               tool_names=(), grammar=None, stream=None):
         """Writes the packed allow-mask into d_mask (torch uint32-compatible int32 tensor of
         ceil(V/32) words on the GPU); returns 0 when nothing is constrained, else 1."""
-        keep = []
-
-        def buf(b):
-            a = np.frombuffer(b or b"\0", np.uint8).copy()
-            keep.append(a)
-            return _np_ptr(a)
-
-        names = [bytes(n) for n in tool_names]
-        name_ptrs = (ctypes.c_void_p * max(len(names), 1))(*[buf(n) for n in names])
-        name_lens = np.array([len(n) for n in names] or [0], np.int64)
         g = None if grammar is None else (grammar.encode() if isinstance(grammar, str) else bytes(grammar))
-        c = Constraint(int(bool(json_object)), int(tool_choice), buf(tool_name), len(tool_name),
-                       ctypes.cast(name_ptrs, ctypes.c_void_p), _np_ptr(name_lens), len(names),
-                       None if g is None else buf(g), 0 if g is None else len(g))
-        sf = np.frombuffer(so_far or b"\0", np.uint8).copy()
+        key = (bool(json_object), int(tool_choice), bytes(tool_name), tuple(bytes(n) for n in tool_names), g)
+        cached = self._prepared.get(key) if hasattr(self, "_prepared") else None
+        if cached is None:  # the constraint struct and the arrays it points into, kept per key
+            keep = []
+
+            def buf(b):
+                a = np.frombuffer(b or b"\0", np.uint8).copy()
+                keep.append(a)
+                return _np_ptr(a)
+
+            names = list(key[3])
+            name_ptrs = (ctypes.c_void_p * max(len(names), 1))(*[buf(n) for n in names])
+            name_lens = np.array([len(n) for n in names] or [0], np.int64)
+            keep += [name_ptrs, name_lens]
+            c = Constraint(int(key[0]), key[1], buf(key[2]), len(key[2]), ctypes.cast(name_ptrs, ctypes.c_void_p),
+                           _np_ptr(name_lens), len(names), None if g is None else buf(g), 0 if g is None else len(g))
+            if not hasattr(self, "_prepared") or len(self._prepared) > 64:
+                self._prepared = {}
+            cached = self._prepared[key] = (c, keep)
+        c = cached[0]
+        sf = np.frombuffer(so_far or b"\0", np.uint8)
         flag = ctypes.c_int32(-1)
         if stream is None:
             import torch

@@ -216,24 +216,47 @@ struct MaskArgs {
     Tables t;
 };
 
-// One thread per id; a wave's 64 verdicts become two mask words by ballot.
+constexpr uint32_t STAGE = 8192;  // bytes of a block's pieces staged in LDS
+
+// One thread per id; a wave's 64 verdicts become two mask words by ballot. The block's
+// pieces are contiguous: their bytes (16-byte aligned span, up to STAGE) are copied to LDS
+// with coalesced 16-byte loads, so each thread then walks its piece without a dependent
+// global load per byte; bytes past the staged span are read from global memory.
 __global__ __launch_bounds__(BLOCK) void k_mask(const MaskArgs a) {
-    const int64_t id = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    __shared__ uint4 stage4[STAGE / 16];
+    const uint8_t* stage = reinterpret_cast<const uint8_t*>(stage4);
+    const int64_t first = (int64_t)blockIdx.x * BLOCK;
+    const int64_t id = first + threadIdx.x;
     bool ok = false;
+    uint32_t b0 = 0, b1 = 0, lo = 0, n_st = 0;
+    if (a.mode == M_SCAN) {
+        const int64_t last = first + BLOCK < a.V ? first + BLOCK : a.V;
+        if (id < a.V) {
+            b0 = a.off[id];
+            b1 = a.off[id + 1];
+        }
+        // the buffer holds 16 bytes of padding past the text, so the aligned span is inside it
+        lo = a.off[first] & ~15u;
+        const uint32_t hi = (a.off[last] + 15u) & ~15u;
+        n_st = hi - lo < STAGE ? hi - lo : STAGE;
+        const uint4* src = reinterpret_cast<const uint4*>(a.bytes + lo);
+        for (uint32_t i = threadIdx.x; i < n_st / 16; i += BLOCK) stage4[i] = src[i];
+        __syncthreads();
+    }
     if (id < a.V) {
         ok = true;
         if (a.mode == M_SCAN) {
-            const uint32_t b0 = a.off[id], b1 = a.off[id + 1];
+            auto byte_at = [&](uint32_t i) -> uint32_t { return i - lo < n_st ? stage[i - lo] : a.bytes[i]; };
             if (a.lit_on) {
                 const uint32_t n = b1 - b0;
                 ok = a.lit_ok && (int64_t)n <= (int64_t)a.t.lit_rem && (int32_t)n <= a.t.lit_len;
-                for (uint32_t i = 0; ok && i < n; i++) ok = a.bytes[b0 + i] == a.t.bytes[a.t.lit_off + i];
+                for (uint32_t i = 0; ok && i < n; i++) ok = byte_at(b0 + i) == a.t.bytes[a.t.lit_off + i];
             }
             if (ok && a.json_on) {
                 JState js = a.j0;
                 NState ns = a.n0;
                 for (uint32_t i = b0; i < b1; i++) {
-                    const uint32_t c = a.bytes[i];
+                    const uint32_t c = byte_at(i);
                     j_step(js, c);
                     if (a.tool_on) n_step(ns, c, a.t);
                 }
@@ -391,7 +414,7 @@ int bfi_mask_set_vocab(bfi_mask_ctx* ctx, const uint8_t* bytes, const int64_t* o
         maxp = n > maxp ? n : maxp;
     }
     const int64_t total = offsets[n_vocab];
-    if (total > (int64_t)0xFFFFFFFFll) return fail(ctx, BFI_SMP_EINVAL, "vocabulary text above 4 GiB");
+    if (total > (int64_t)0xFFFFFF00ll) return fail(ctx, BFI_SMP_EINVAL, "vocabulary text of 4 GiB or more");
     if (total > 0 && !bytes) return fail(ctx, BFI_SMP_EINVAL, "bytes is NULL");
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return hfail(ctx, e, "hipSetDevice");
@@ -402,7 +425,8 @@ int bfi_mask_set_vocab(bfi_mask_ctx* ctx, const uint8_t* bytes, const int64_t* o
     ctx->V = -1;
     std::vector<uint32_t> off32((size_t)n_vocab + 1);
     for (int64_t i = 0; i <= n_vocab; i++) off32[(size_t)i] = (uint32_t)offsets[i];
-    if ((e = hipMalloc((void**)&ctx->d_bytes, (size_t)(total > 0 ? total : 1))) != hipSuccess ||
+    // 16 bytes of padding: k_mask stages 16-byte aligned spans of the text
+    if ((e = hipMalloc((void**)&ctx->d_bytes, (size_t)total + 16)) != hipSuccess ||
         (e = hipMalloc((void**)&ctx->d_off, off32.size() * sizeof(uint32_t))) != hipSuccess)
         return fail(ctx, BFI_SMP_ENOMEM, "vocabulary allocation failed: %s", hipGetErrorString(e));
     if (total > 0 && (e = hipMemcpy(ctx->d_bytes, bytes, (size_t)total, hipMemcpyHostToDevice)) != hipSuccess)

@@ -186,3 +186,32 @@ def to_device(cfg: dict, device="cuda:0") -> dict:
         d["out_accepted"] = torch.zeros(cfg["n_seq"], dtype=torch.int32, device=device)
         d["out_next"] = torch.zeros(cfg["n_seq"], dtype=torch.int32, device=device)
     return d
+
+
+# ---- the allow-mask producer's workload (include/bfi_mask.h) ------------------------------
+
+MASK_SO_FAR = b'{"name": "lookup", "arguments": {"query": "weather in '
+MASK_TOOLS = dict(tool_choice=3, tool_name=b"lookup", tool_names=[b"lookup", b"search", b"list_files"])
+
+
+def synthetic_vocab(V: int = 151936, seed: int = 0) -> list:
+    """V decoded pieces shaped like a BPE vocabulary: 1-16 bytes (mean about 6), mostly
+    letters with a leading space, plus digits, JSON punctuation and some UTF-8 (no tokenizer
+    files are available, so the texts are synthetic)."""
+    rng = np.random.default_rng(seed)
+    letters = np.frombuffer(b"abcdefghijklmnopqrstuvwxyz", np.uint8)
+    punct = [b"{", b"}", b"[", b"]", b'"', b":", b",", b"\\", b'":', b'{"', b'"}', b"\n", b"  ", b"\t"]
+    lens = np.clip(rng.geometric(0.18, V), 1, 16)
+    out = []
+    for i in range(V):
+        r = rng.random()
+        if r < 0.08:
+            out.append(punct[rng.integers(len(punct))] + (b'"' if rng.random() < 0.2 else b""))
+        elif r < 0.12:
+            out.append(str(int(rng.integers(0, 1000))).encode())
+        elif r < 0.15:
+            out.append("é✓日本ü"[rng.integers(5)].encode() * int(rng.integers(1, 3)))
+        else:
+            w = bytes(letters[rng.integers(0, 26, int(lens[i]))])
+            out.append((b" " + w) if rng.random() < 0.5 else w)
+    return out
