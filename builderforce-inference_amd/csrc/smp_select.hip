@@ -461,13 +461,17 @@ __device__ __forceinline__ void transform_raw(const Smem& sm, const RowCtx& C, c
         if (id0 >= c1) continue;  // all -inf already
         const uint32_t mb = C.mrow ? (r.mw[q] >> (id0 & 31)) & em : em;
         const uint32_t pb = !C.pen_on ? 0u : S.hash ? pen_bits(sm, S, id0, EPV) : (r.pw[q] >> (id0 & 31)) & em;
-        if (pb) {  // rare: an id of the history in this vector
+        // Every vector takes the vector path; the few history ids (per lane, so a wave runs
+        // an element's fix-up only when one of its lanes has that element in the history) are
+        // then recomputed from their raw logits.
+        float xr[EPV];
+#pragma unroll
+        for (int e = 0; e < EPV; e++) xr[e] = x[q][e];
+        raw_vector<EPV>(C, x[q], mb);
+        if (pb) {
 #pragma unroll
             for (int e = 0; e < EPV; e++)
-                x[q][e] = ((pb >> e) & 1u) ? pen_value(C, x[q][e], (mb >> e) & 1u, pen_count(sm, S, C, id0 + e))
-                                           : raw_value(C, x[q][e], (mb >> e) & 1u);
-        } else {
-            raw_vector<EPV>(C, x[q], mb);
+                if ((pb >> e) & 1u) x[q][e] = pen_value(C, xr[e], (mb >> e) & 1u, pen_count(sm, S, C, id0 + e));
         }
     }
 }
