@@ -68,10 +68,6 @@ struct __align__(16) Smem {
     uint64_t r64[NWAVE];
     uint64_t r64b[NWAVE];
     uint32_t misc[8];
-    // value buckets spec_lo..spec_hi of the row, complete (every element), gathered with an
-    // earlier query for a query expected to follow; spec_lo > spec_hi when empty
-    uint64_t spec[NSPEC];
-    uint32_t spec_n, spec_lo, spec_hi;
     uint32_t fx[8];   // the fast finish's row values
     uint64_t tr[16];  // phase timestamps of this workgroup (diagnostics)
     // row aggregates built with LDS atomics (integer, so independent of the order)
@@ -86,6 +82,11 @@ struct __align__(16) Smem {
         uint32_t nd;      // history ids that hold their chunk's maximum
         uint32_t kth;     // ord32 of the k-th largest chunk maximum (top-k rows, k <= chunks)
     } ag;
+    // value buckets spec_lo..spec_hi of the row, complete (every element), gathered with an
+    // earlier query for a query expected to follow; spec_lo > spec_hi when empty. Last, so
+    // that the fields the fast finish uses keep their offsets and alignment.
+    uint32_t spec_n, spec_lo, spec_hi, spec_pad;
+    uint64_t spec[NSPEC];
 };
 
 constexpr double FIX52 = 4503599627370496.0;  // 2^52: fixed-point scale of the history corrections
