@@ -150,3 +150,16 @@ def test_c2_algorithmic_bytes_match_the_derivation():
     # logits + 512-id histories + offsets + 32-byte params + u + token
     want = B * V * 4 + B * 512 * 4 + (B + 1) * 8 + B * 32 + B * 4 + B * 4
     assert workloads.algorithmic_bytes(cfg) == want
+
+
+def test_mask_entry_points_reject_bad_arguments_without_a_device():
+    """include/bfi_mask.h: argument errors come back as status codes (no GPU work)."""
+    L = bfi_smp.lib()
+    assert L.bfi_mask_error(None) == b"null context"
+    assert L.bfi_mask_set_vocab(None, None, None, 0) == 1  # BFI_SMP_EINVAL
+    c = bfi_smp.Constraint()
+    assert L.bfi_mask_build(None, None, 0, ctypes.byref(c), None, None, None) == 1
+    h = ctypes.c_void_p()
+    rc = L.bfi_mask_create(-1, ctypes.byref(h))
+    assert rc != 0 and not h.value
+    L.bfi_mask_destroy(None)
