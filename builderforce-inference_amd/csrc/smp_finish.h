@@ -452,6 +452,13 @@ __device__ __forceinline__ bool select_fast(const KArgs& a, SM& sm, int row, F r
     mine.raw_m = -__builtin_inff();
     mine.raw_arg = 0xFFFFFFFFu;
     if (tid < nc) mine = a.parts[(int64_t)row * nc + tid];
+    // The first BLOCK / nc candidates of every chunk go out with the chunk results (thread t:
+    // chunk t / per, slot t % per); when no chunk hands over more, they are the whole list and
+    // the gather needs no second round trip. Slots past a chunk's count are ignored.
+    const uint32_t per = (uint32_t)BLOCK / (uint32_t)nc;
+    const uint32_t sc = (uint32_t)tid / per, sj = (uint32_t)tid % per;
+    Cand spec{0u, -__builtin_inff()};
+    if (sc < (uint32_t)nc) spec = a.cands[((int64_t)row * nc + sc) * CAND_CAP + sj];
     const RowCtx C = row_ctx();
     if (!C.active) return true;  // a verify row past its draft: nothing to emit
     BFI_FTRACE(a, sm, 8);
@@ -462,7 +469,7 @@ __device__ __forceinline__ bool select_fast(const KArgs& a, SM& sm, int row, F r
     uint32_t* fx = sm.fx;
     if (wave_id() == 0) {
         const bool in = lane < nc;
-        uint32_t status = 0;  // 0: list, 1: token (greedy), 2: leave to k_select
+        uint32_t status = 0;  // 0: list, 1: token (greedy), 2: leave to k_select, 3: list, prefetched
         if (C.greedy) {  // sample.rs:369-371, 429-439: argmax of the penalized logits
             const ArgMax am = argmax_of_key(wave_max_u64(in ? argmax_key(mine.m, mine.arg) : 0ull));
             status = 1;
@@ -479,6 +486,7 @@ __device__ __forceinline__ bool select_fast(const KArgs& a, SM& sm, int row, F r
                 const float th_m = minp_bound(C, M);
                 const float th = fmaxf(wave_max(in ? mine.theta : -__builtin_inff()), th_m);
                 const uint32_t take = in ? chunk_take(mine, th) : 0u;
+                if (__ballot(take > per) == 0ull) status = 3;
                 const uint32_t incl = wave_scan_incl(take, 0u, [](uint32_t x, uint32_t y) { return x + y; });
                 if (in) sm.cpre[lane] = incl - take;
                 const ArgMax rawmax = C.min_p > 1.0f
@@ -509,8 +517,16 @@ __device__ __forceinline__ bool select_fast(const KArgs& a, SM& sm, int row, F r
     const float M = __uint_as_float(fx[F_M]), S = __uint_as_float(fx[F_S]);
     const float th = __uint_as_float(fx[F_TH]), th_m = __uint_as_float(fx[F_THM]);
     const ArgMax rawmax{__uint_as_float(fx[F_RAWV]), fx[F_RAWI]};
-    for (uint32_t b0 = 0; b0 < sm.cpre[nc]; b0 += GU * BLOCK)  // uniform trip count
-        append_cands(sm, C, load_cands(a, sm, row, nc, b0), th, sorted, no_exclusion);
+    if (status == 3) {
+        CandBatch B;
+#pragma unroll
+        for (int g = 0; g < GU; g++) B.cd[g] = Cand{0u, -__builtin_inff()};
+        if (sc < (uint32_t)nc && sj < sm.cpre[sc + 1] - sm.cpre[sc]) B.cd[0] = spec;
+        append_cands(sm, C, B, th, sorted, no_exclusion);
+    } else {
+        for (uint32_t b0 = 0; b0 < sm.cpre[nc]; b0 += GU * BLOCK)  // uniform trip count
+            append_cands(sm, C, load_cands(a, sm, row, nc, b0), th, sorted, no_exclusion);
+    }
     __syncthreads();
     BFI_FTRACE(a, sm, 3);
     if (a.t_stats && tid == 0) {
