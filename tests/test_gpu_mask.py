@@ -3,7 +3,8 @@
 Cases: the reference's constraint tests (sample.rs:505-581), small vocabularies of
 structural pieces under every prefix of tool-call texts for json_object / required / named
 tool choices and literal grammars, tool-name tables (names that prefix each other, 64
-names), id unions, and a full 151,936-piece vocabulary."""
+names), id unions, a full 151,936-piece vocabulary, and pieces long enough to overflow the
+text a block stages in LDS."""
 import random
 
 import numpy as np
@@ -130,3 +131,20 @@ def test_full_vocabulary(mp):
     check(mp, pieces, b'{"name": "lo', "full-named", tool_choice=K.TOOL_NAMED, tool_name=b"lookup",
           tool_names=[b"lookup", b"list"])
     check(mp, pieces, b'{"name": "lookup", "arguments": {"q": "', "full-json", json_object=True)
+
+
+def test_long_pieces_past_the_staged_span(mp):
+    """Pieces of thousands of bytes: a block's text exceeds the 8 KB staged in LDS, so the
+    threads read the rest from global memory; also an empty vocabulary slot and a 3000-byte
+    literal (its tail, cut to the longest piece, travels in the kernel arguments)."""
+    rng = random.Random(15)
+    pieces = rand_pieces(rng, 600)
+    for i in range(0, 600, 37):
+        body = b"".join(rng.choice([b" ", b"{", b"}", b'"', b"\\", b"name", b'"name": "l', b"x"]) for _ in range(900))
+        pieces[i] = body
+    pieces[5] = b""
+    for so_far in (b"", b"{", b'{"name": "l', b'{"a": "'):
+        check(mp, pieces, so_far, "long-json", json_object=True)
+        check(mp, pieces, so_far, "long-named", tool_choice=K.TOOL_NAMED, tool_name=b"lookup", tool_names=[b"lookup"])
+    lit = "{" * 3000
+    check(mp, pieces, b"{{", "long-literal", grammar=f'root ::= "{lit}"')
