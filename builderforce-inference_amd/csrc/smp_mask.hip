@@ -199,11 +199,12 @@ __host__ __device__ inline bool n_accept(const NState& s, const Tables& t) {
     }
 }
 
-enum : int32_t { M_ALL = 0, M_SCAN = 1 };
+enum : int32_t { M_ALL = 0, M_SCAN = 1, M_NONE = 2 };
 
 struct MaskArgs {
     const uint8_t* bytes;
     const uint32_t* off;
+    const uint4* rows;  // per id: up to 15 bytes of its piece, byte 15 its length (LONG: longer)
     uint32_t* mask;
     int64_t V;
     int32_t mode;
@@ -216,46 +217,38 @@ struct MaskArgs {
     Tables t;
 };
 
-constexpr uint32_t STAGE = 8192;  // bytes of a block's pieces staged in LDS
+constexpr uint32_t LONG = 0xFFu;  // length byte of a piece longer than 15 bytes
 
-// One thread per id; a wave's 64 verdicts become two mask words by ballot. The block's
-// pieces are contiguous: their bytes (16-byte aligned span, up to STAGE) are copied to LDS
-// with coalesced 16-byte loads, so each thread then walks its piece without a dependent
-// global load per byte; bytes past the staged span are read from global memory.
+// One thread per id; a wave's 64 verdicts become two mask words by ballot. A piece of at most
+// 15 bytes comes with its length in one 16-byte row (consecutive ids, consecutive rows: one
+// coalesced load per thread, no offset lookup first); longer pieces are read from the text.
 __global__ __launch_bounds__(BLOCK) void k_mask(const MaskArgs a) {
-    __shared__ uint4 stage4[STAGE / 16];
-    const uint8_t* stage = reinterpret_cast<const uint8_t*>(stage4);
-    const int64_t first = (int64_t)blockIdx.x * BLOCK;
-    const int64_t id = first + threadIdx.x;
+    const int64_t id = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
     bool ok = false;
-    uint32_t b0 = 0, b1 = 0, lo = 0, n_st = 0;
-    if (a.mode == M_SCAN) {
-        const int64_t last = first + BLOCK < a.V ? first + BLOCK : a.V;
-        if (id < a.V) {
-            b0 = a.off[id];
-            b1 = a.off[id + 1];
-        }
-        // the buffer holds 16 bytes of padding past the text, so the aligned span is inside it
-        lo = a.off[first] & ~15u;
-        const uint32_t hi = (a.off[last] + 15u) & ~15u;
-        n_st = hi - lo < STAGE ? hi - lo : STAGE;
-        const uint4* src = reinterpret_cast<const uint4*>(a.bytes + lo);
-        for (uint32_t i = threadIdx.x; i < n_st / 16; i += BLOCK) stage4[i] = src[i];
-        __syncthreads();
-    }
-    if (id < a.V) {
+    if (id < a.V && a.mode != M_NONE) {
         ok = true;
         if (a.mode == M_SCAN) {
-            auto byte_at = [&](uint32_t i) -> uint32_t { return i - lo < n_st ? stage[i - lo] : a.bytes[i]; };
+            const uint4 row = a.rows[id];
+            const uint32_t len = row.w >> 24;
+            uint32_t b0 = 0, n = len;
+            if (len == LONG) {
+                b0 = a.off[id];
+                n = a.off[id + 1] - b0;
+            }
+            auto byte_at = [&](uint32_t i) -> uint32_t {
+                if (len == LONG) return a.bytes[b0 + i];
+                const uint32_t wsel = i >> 2;
+                const uint32_t word = wsel == 0 ? row.x : wsel == 1 ? row.y : wsel == 2 ? row.z : row.w;
+                return (word >> (8 * (i & 3u))) & 0xFFu;
+            };
             if (a.lit_on) {
-                const uint32_t n = b1 - b0;
                 ok = a.lit_ok && (int64_t)n <= (int64_t)a.t.lit_rem && (int32_t)n <= a.t.lit_len;
-                for (uint32_t i = 0; ok && i < n; i++) ok = byte_at(b0 + i) == a.t.bytes[a.t.lit_off + i];
+                for (uint32_t i = 0; ok && i < n; i++) ok = byte_at(i) == a.t.bytes[a.t.lit_off + i];
             }
             if (ok && a.json_on) {
                 JState js = a.j0;
                 NState ns = a.n0;
-                for (uint32_t i = b0; i < b1; i++) {
+                for (uint32_t i = 0; i < n; i++) {
                     const uint32_t c = byte_at(i);
                     j_step(js, c);
                     if (a.tool_on) n_step(ns, c, a.t);
@@ -356,6 +349,7 @@ struct bfi_mask_ctx {
     std::string err;
     uint8_t* d_bytes = nullptr;
     uint32_t* d_off = nullptr;
+    uint4* d_rows = nullptr;
     int64_t V = -1;
     int64_t max_piece = 0;
     std::vector<uint32_t> host_mask;  // id unions
@@ -397,6 +391,7 @@ void bfi_mask_destroy(bfi_mask_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->d_bytes) (void)hipFree(ctx->d_bytes);
     if (ctx->d_off) (void)hipFree(ctx->d_off);
+    if (ctx->d_rows) (void)hipFree(ctx->d_rows);
     delete ctx;
 }
 
@@ -420,12 +415,14 @@ int bfi_mask_set_vocab(bfi_mask_ctx* ctx, const uint8_t* bytes, const int64_t* o
     if (e != hipSuccess) return hfail(ctx, e, "hipSetDevice");
     if (ctx->d_bytes) (void)hipFree(ctx->d_bytes);
     if (ctx->d_off) (void)hipFree(ctx->d_off);
+    if (ctx->d_rows) (void)hipFree(ctx->d_rows);
     ctx->d_bytes = nullptr;
     ctx->d_off = nullptr;
+    ctx->d_rows = nullptr;
     ctx->V = -1;
     std::vector<uint32_t> off32((size_t)n_vocab + 1);
     for (int64_t i = 0; i <= n_vocab; i++) off32[(size_t)i] = (uint32_t)offsets[i];
-    // 16 bytes of padding: k_mask stages 16-byte aligned spans of the text
+    // 16 bytes of padding past the text
     if ((e = hipMalloc((void**)&ctx->d_bytes, (size_t)total + 16)) != hipSuccess ||
         (e = hipMalloc((void**)&ctx->d_off, off32.size() * sizeof(uint32_t))) != hipSuccess)
         return fail(ctx, BFI_SMP_ENOMEM, "vocabulary allocation failed: %s", hipGetErrorString(e));
@@ -434,6 +431,22 @@ int bfi_mask_set_vocab(bfi_mask_ctx* ctx, const uint8_t* bytes, const int64_t* o
     if ((e = hipMemcpy(ctx->d_off, off32.data(), off32.size() * sizeof(uint32_t), hipMemcpyHostToDevice)) !=
         hipSuccess)
         return hfail(ctx, e, "hipMemcpy(vocabulary offsets)");
+    // the 16-byte rows: up to 15 bytes of the piece, its length in the last byte
+    std::vector<uint8_t> rows((size_t)(n_vocab > 0 ? n_vocab : 1) * 16, 0);
+    for (int64_t i = 0; i < n_vocab; i++) {
+        const int64_t n = offsets[i + 1] - offsets[i];
+        uint8_t* r = rows.data() + (size_t)i * 16;
+        if (n <= 15) {
+            if (n > 0) memcpy(r, bytes + offsets[i], (size_t)n);
+            r[15] = (uint8_t)n;
+        } else {
+            r[15] = (uint8_t)LONG;
+        }
+    }
+    if ((e = hipMalloc((void**)&ctx->d_rows, rows.size())) != hipSuccess)
+        return fail(ctx, BFI_SMP_ENOMEM, "vocabulary rows allocation failed: %s", hipGetErrorString(e));
+    if ((e = hipMemcpy(ctx->d_rows, rows.data(), rows.size(), hipMemcpyHostToDevice)) != hipSuccess)
+        return hfail(ctx, e, "hipMemcpy(vocabulary rows)");
     ctx->V = n_vocab;
     ctx->max_piece = maxp;
     return BFI_SMP_OK;
@@ -462,6 +475,7 @@ int bfi_mask_build(bfi_mask_ctx* ctx, const uint8_t* so_far, int64_t so_far_len,
     memset(&a, 0, sizeof a);
     a.bytes = ctx->d_bytes;
     a.off = ctx->d_off;
+    a.rows = ctx->d_rows;
     a.mask = d_mask;
     a.V = V;
     a.mode = M_SCAN;
@@ -534,8 +548,14 @@ int bfi_mask_build(bfi_mask_ctx* ctx, const uint8_t* so_far, int64_t so_far_len,
             j_step(a.j0, so_far[i]);
             if (a.tool_on) n_step(a.n0, so_far[i], t);
         }
-        // past a decision in so_far the verdict is the same for every piece; the kernel still
-        // runs the (then absorbing) automata over each piece
+        // Past a decision in so_far the verdict no longer depends on the piece: a rejected
+        // object or name rejects every id; a decided name leaves only the object check.
+        if (a.json_on && a.j0.phase == J_DEAD) a.mode = M_NONE;
+        if (a.tool_on && (a.n0.phase == N_DONE || a.n0.phase == N_INVALID)) {
+            if (n_accept(a.n0, t)) a.tool_on = 0;
+            else a.mode = M_NONE;
+        }
+        if (a.lit_on && !a.lit_ok) a.mode = M_NONE;
     }
     if (V == 0) return BFI_SMP_OK;
     const unsigned grid = (unsigned)((V + BLOCK - 1) / BLOCK);

@@ -3,8 +3,7 @@
 Cases: the reference's constraint tests (sample.rs:505-581), small vocabularies of
 structural pieces under every prefix of tool-call texts for json_object / required / named
 tool choices and literal grammars, tool-name tables (names that prefix each other, 64
-names), id unions, a full 151,936-piece vocabulary, and pieces long enough to overflow the
-text a block stages in LDS."""
+names), id unions, a full 151,936-piece vocabulary, and pieces of thousands of bytes."""
 import random
 
 import numpy as np
@@ -133,10 +132,10 @@ def test_full_vocabulary(mp):
     check(mp, pieces, b'{"name": "lookup", "arguments": {"q": "', "full-json", json_object=True)
 
 
-def test_long_pieces_past_the_staged_span(mp):
-    """Pieces of thousands of bytes: a block's text exceeds the 8 KB staged in LDS, so the
-    threads read the rest from global memory; also an empty vocabulary slot and a 3000-byte
-    literal (its tail, cut to the longest piece, travels in the kernel arguments)."""
+def test_long_pieces(mp):
+    """Pieces of thousands of bytes (read from the text, not the 16-byte rows), an empty
+    vocabulary slot, and a 3000-byte literal (its tail, cut to the longest piece, travels in
+    the kernel arguments)."""
     rng = random.Random(15)
     pieces = rand_pieces(rng, 600)
     for i in range(0, 600, 37):
