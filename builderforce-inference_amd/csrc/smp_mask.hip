@@ -4,7 +4,8 @@
 // concatenation (sample.rs:82-89: V scans of |so_far| + |piece| bytes per step). Here the
 // checks of `token_allowed` (sample.rs:92-107) are byte automata: the host runs them once over
 // `so_far`, and one GPU thread per id continues the resulting state over its piece, so a step
-// reads each piece once (about 1 MB for a 152K vocabulary). Integer work, no MFMA.
+// reads each piece once (a 16-byte row per id: about 2.5 MB for a 152K vocabulary). Integer
+// work, no MFMA.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
