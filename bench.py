@@ -159,7 +159,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's path runs on a single MI355X "
-              "(rows shard across GPUs with no exchange; see DESIGN.md). Use --gpus 1.", file=sys.stderr)
+              "(rows shard across GPUs with no exchange between them). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
