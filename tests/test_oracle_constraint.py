@@ -143,3 +143,41 @@ def test_grammar_parsers():
     assert K.parse_literal_root('root ::= ab') is None
     assert K.parse_literal_root('root ::= "ab') is None
     assert K.rust_trim("\x1c a \x1c") == "\x1c a \x1c"  # not White_Space in Rust (Python strips it)
+
+
+# ---- brute force against an independent statement of the brace/string scan --------------
+
+
+def _prefix_ok_independent(b: bytes) -> bool:
+    """json_object_prefix_ok stated differently: strings (closed, or open at the end) collapse
+    to one byte by a regular expression, then the running bracket depth over what is left
+    must stay positive until it first returns to zero, after which only ASCII whitespace may
+    follow."""
+    import itertools
+    import re
+
+    s = b.lstrip(b" \t\n\x0c\r")
+    if not s:
+        return True
+    if s[:1] != b"{":
+        return False
+    t = re.sub(rb'"(?:\\.|\\$|[^"\\])*(?:"|$)', b"S", s, flags=re.S)
+    steps = [1 if c in b"{[" else -1 if c in b"}]" else 0 for c in t]
+    depth = list(itertools.accumulate(steps))
+    for i, d in enumerate(depth):
+        if d <= 0:
+            return all(c in b" \t\n\x0c\r" for c in t[i + 1:])
+    return True
+
+
+def test_json_object_prefix_ok_brute_force():
+    import itertools
+
+    alphabet = [b" ", b"{", b"}", b"[", b"]", b'"', b"\\", b"a", b"\x0b"]
+    n = 0
+    for length in range(0, 7):
+        for combo in itertools.product(alphabet, repeat=length):
+            b = b"".join(combo)
+            assert K.json_object_prefix_ok(b) == _prefix_ok_independent(b), b
+            n += 1
+    assert n > 500000
