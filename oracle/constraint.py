@@ -5,9 +5,12 @@ Strings are handled as UTF-8 bytes, as the reference's `str` methods compare the
 function cites the reference lines it follows. Only tests/ import this module.
 
 Pinned by: the reference's constraint tests (sample.rs:505-581, restated as known answers in
-tests/test_oracle_constraint.py), Python's json module on complete objects and on every
-prefix of them, and brute force over short strings of the structural characters (an
-independent recursive statement of the brace/string scan).
+tests/test_oracle_constraint.py); for json_object_prefix_ok, Python's json module on complete
+objects and on every prefix of them, and brute force over all strings of up to six structural
+characters against an independent statement of the scan (strings collapsed by a regular
+expression, the depth as a running sum); for json_name_so_far, tool_call_prefix_ok and the
+grammar parsers, hand-derived cases (the key's restart after a non-colon, escapes, prefixes
+of several names, Rust's whitespace set).
 """
 from __future__ import annotations
 
