@@ -16,13 +16,13 @@
 
 namespace bfi {
 hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
-hipError_t launch_select(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+hipError_t launch_row(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 }
 
 struct bfi_smp_ctx {
     int device = 0;
     std::string err;
-    char* ws = nullptr;  // parts | cands | row_res | row_pen | row_hist
+    char* ws = nullptr;  // parts | vhist | row_res | row_pen | spill
     size_t ws_size = 0;
     uint32_t* ctr = nullptr;  // seq_ctr, kept zero between launches
     size_t ctr_words = 0;
@@ -34,7 +34,7 @@ struct bfi_smp_ctx {
     uint64_t* trace = nullptr;
     size_t trace_words = 0, trace_used = 0;
     bool tracing = false;
-    // profiling: per launch, start/stop events recorded in the dispatches of k_stream and k_select
+    // profiling: per launch, start/stop events recorded in the dispatches of k_stream and k_row
     bool profiling = false;
     std::vector<hipEvent_t> ev_pool;
     size_t ev_used = 0;
@@ -77,11 +77,6 @@ struct DeviceGuard {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-int ceil_log2(int64_t v) {
-    int b = 0;
-    while ((int64_t(1) << b) < v) b++;
-    return b;
-}
 
 // Launch shape: 16-byte vectors per thread -> chunk of BLOCK*VEC*EPV elements. The largest
 // chunk that still gives >= 1024 workgroups (4 per CU on 256 CUs); at most 256 chunks/row.
@@ -106,22 +101,22 @@ bool choose_shape(int64_t n_rows, int64_t V, int bf16, Shape& s) {
 }
 
 struct Layout {
-    size_t parts, cands, row_res, row_pen, row_hist, total;
+    size_t parts, vhist, row_res, row_pen, spill, total;
 };
 
-Layout layout(int64_t n_rows, const Shape& s, int bm_words) {
+Layout layout(int64_t n_rows, int64_t V, const Shape& s, int bm_words) {
     Layout L;
     size_t off = 0;
     L.parts = off;
     off = align_up(off + (size_t)n_rows * s.n_chunks * sizeof(bfi::ChunkPart), 256);
-    L.cands = off;
-    off = align_up(off + (size_t)n_rows * s.n_chunks * bfi::CAND_CAP * sizeof(bfi::Cand), 256);
+    L.vhist = off;
+    off = align_up(off + (size_t)n_rows * s.n_chunks * bfi::HBINS * sizeof(uint32_t), 256);
     L.row_res = off;
     off = align_up(off + (size_t)n_rows * 2 * sizeof(uint32_t), 256);
     L.row_pen = off;
     off = align_up(off + (size_t)n_rows * (2 * (size_t)bm_words + bfi::GDCAP) * sizeof(uint32_t), 256);
-    L.row_hist = off;
-    off = align_up(off + (size_t)n_rows * bfi::NVB * 2 * sizeof(uint64_t), 256);
+    L.spill = off;
+    off = align_up(off + (size_t)n_rows * 4 * (size_t)V * sizeof(uint64_t), 256);
     L.total = off;
     return L;
 }
@@ -221,7 +216,7 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     Shape s;
     if (!choose_shape(c.n_rows, c.V, c.dtype == BFI_SMP_BF16, s))
         return fail(ctx, BFI_SMP_EINVAL, "no launch shape for n_vocab %lld", (long long)c.V);
-    const Layout L = layout(c.n_rows, s, bm_words);
+    const Layout L = layout(c.n_rows, c.V, s, bm_words);
     const size_t ctr_words = verify ? (size_t)c.n_seq : 1;
     int rc = ensure_ws(ctx, L.total, ctr_words, stream);
     if (rc) return rc;
@@ -236,7 +231,6 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     a.chunk = s.chunk;
     const size_t esz = c.dtype == BFI_SMP_BF16 ? 2 : 4;
     a.vec_ok = ((uintptr_t)c.logits % 16 == 0) && ((size_t)c.row_stride * esz % 16 == 0);
-    a.fix_bits = 62 - ceil_log2(c.V);
     a.params = c.params;
     a.hist = c.hist;
     a.hist_off = c.hist_off;
@@ -259,10 +253,10 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     a.out_accepted = c.out_acc;
     a.out_next = c.out_next;
     a.parts = (bfi::ChunkPart*)(ctx->ws + L.parts);
-    a.cands = (bfi::Cand*)(ctx->ws + L.cands);
+    a.vhist = (uint32_t*)(ctx->ws + L.vhist);
     a.row_res = (uint32_t*)(ctx->ws + L.row_res);
     a.row_pen = (uint32_t*)(ctx->ws + L.row_pen);
-    a.row_hist = (uint64_t*)(ctx->ws + L.row_hist);
+    a.spill = (uint64_t*)(ctx->ws + L.spill);
     a.seq_ctr = ctx->ctr;
     a.bm_words = bm_words;
     a.trace = nullptr;
@@ -300,8 +294,8 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     hipError_t e = hipSuccess;
     if ((e = bfi::launch_stream(a, bf16, s.vec, stream, ev[0], ev[1])) != hipSuccess)
         return hip_fail(ctx, e, "k_stream launch");
-    if ((e = bfi::launch_select(a, bf16, stream, ev[2], ev[3])) != hipSuccess)
-        return hip_fail(ctx, e, "k_select launch");
+    if ((e = bfi::launch_row(a, bf16, stream, ev[2], ev[3])) != hipSuccess)
+        return hip_fail(ctx, e, "k_row launch");
     return BFI_SMP_OK;
 }
 

@@ -23,40 +23,22 @@ constexpr int NWAVE = BLOCK / WAVE;
 constexpr int CHUNK_MAX = 8192;        // logits elements per workgroup (stream phase)
 constexpr int NCMAX = 256;             // chunks per row
 constexpr int PREPEN_H = 1024;         // histories up to this length are applied by the stream pass
-constexpr int CAND_CAP = 2048;         // candidates one chunk may hand to the combine
-constexpr int NMAX = 2048;             // combine sort capacity (power of two)
-constexpr int NBUCKET = 1024;          // radix buckets (10-bit key digits) of the fallback select
-constexpr int NVB = 2048;              // value buckets of the row select (1/32 wide below the row max)
-constexpr int DCAP = 1024;             // distinct history ids counted per chunk in LDS
-constexpr int GDCAP = 4096;            // distinct history ids counted per row (global scratch)
-constexpr int HSLOTS_LOG2 = 11;
-constexpr int HSLOTS = 1 << HSLOTS_LOG2;  // LDS history hash slots (select kernel)
-constexpr int HMAX = 1536;             // distinct history ids the hash takes (75% load)
-constexpr uint32_t HEMPTY = 0xFFFFFFFFu;
-constexpr uint32_t NCAND_UNBOUNDED = 0xFFFFFFFFu;  // row has no top-k / min-p bound
-constexpr uint32_t NCAND_OVERFLOW = 0xFFFFFFFEu;   // chunk had more than CAND_CAP candidates
+constexpr int GDCAP = 4096;            // distinct history ids counted per row (global tables)
+constexpr int HBINS = 128;             // bins of the stream pass's per-chunk value histogram
+constexpr int HBIN_PER_LOG2 = 8;       // bins per log2-unit below the chunk maximum
 constexpr float F32_EPS = 1.1920928955078125e-07f;  // f32::EPSILON
 
 // Per (row, chunk) result of the streaming pass over the values s = x / T of the masked
 // logits x (greedy: x itself), penalized when the row's context says prepen (else the
-// select kernel corrects the history ids).
+// row kernel applies the history itself).
 struct ChunkPart {
     float m;          // max of s (exact)
     uint32_t arg;     // greedy: first index attaining m
-    double sum;       // sum of stream_term over the chunk (f64 over per-vector f32 sums)
-    uint32_t ncand;   // candidates written, or NCAND_UNBOUNDED / NCAND_OVERFLOW
-    float theta;      // every element of the chunk with finite s >= theta was written
-    float raw_m;      // max of x (the terms' reference point); rows with min_p > 1: of the
-                      // un-penalized masked logits
+    double sum;       // approximate sum of 2^((x - xm) log2(e) / T) over the chunk
+    float xm;         // max of x (the sums' and the histogram's reference point)
+    float raw_m;      // rows with min_p > 1: max of the masked, un-penalized logits
     uint32_t raw_arg; // first index of that maximum (greedy rows and rows with min_p > 1)
     uint32_t pad;
-    uint32_t pad2;
-};
-
-// A candidate of the kept set: its index and x (the select kernel divides by T).
-struct Cand {
-    uint32_t idx;
-    float x;
 };
 
 // Everything a launch needs; passed by value.
@@ -68,9 +50,9 @@ struct KArgs {
     int32_t n_chunks;
     int32_t chunk;  // elements per chunk
     int32_t vec_ok; // rows are 16-byte aligned: vector loads allowed
-    int32_t fix_bits;
+    int32_t pad0;
     const bfi_smp_row_params* params;
-    const uint32_t* hist;
+    const uint32_t* hist;   // penalty histories (token ids)
     const int64_t* hist_off;
     const uint32_t* mask;
     int64_t mask_stride;
@@ -94,13 +76,14 @@ struct KArgs {
     uint32_t* out_next;
     // workspace
     ChunkPart* parts;
-    Cand* cands;
+    uint32_t* vhist;     // per (row, chunk): HBINS counts (top-k / top-p rows)
     uint32_t* seq_ctr;
     uint32_t* row_res;   // verify: 2 words per row {verdict, token}
-    uint32_t* row_pen;   // fallback select: per row bm[bm_words] + pre[bm_words] + cnt[GDCAP]
-    uint64_t* row_hist;  // row select: per row value histogram (mass, count) x NVB
+    uint32_t* row_pen;   // per row: history bitmap[bm_words] + popcount prefix[bm_words] + counts[GDCAP]
+    uint64_t* spill;     // per row: 4 * V keys (the list beyond LDS, its grouped copy, sort scratch)
     int32_t bm_words;
-    uint64_t* trace;  // optional phase timestamps (wall clock) per workgroup
+    int32_t pad1;
+    uint64_t* trace;     // optional phase timestamps (wall clock) per workgroup
 };
 
 // Phase timestamp of a workgroup (diagnostics; no-op without a trace buffer).
@@ -427,6 +410,12 @@ struct ArgMax {
 __device__ __forceinline__ ArgMax argmax_merge(ArgMax a, ArgMax b) {
     if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
     return a;
+}
+// (value, index) as a 64-bit key whose unsigned max is the reference's argmax (largest
+// value, then lowest index; sample.rs:429-439); 0 = none.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) { return ((uint64_t)ord32(v) << 32) | ~i; }
+__device__ __forceinline__ ArgMax argmax_of_key(uint64_t k) {
+    return k ? ArgMax{unord32((uint32_t)(k >> 32)), ~(uint32_t)k} : ArgMax{-__builtin_inff(), 0xFFFFFFFFu};
 }
 __device__ __forceinline__ ArgMax wave_argmax(ArgMax a) {
     // (value, index) packed in 64 bits for the DPP scan; merged with argmax_merge

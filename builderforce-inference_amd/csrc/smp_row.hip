@@ -1,0 +1,1313 @@
+// smp_row.hip — the row pass of the gfx950 token sampler: one workgroup of 1024 threads
+// per row finishes `target()` and `draw()` (sample.rs:326-427, 312-323) or `judge()`
+// (spec.rs:79-97) with the reference's own f32 results.
+//
+// After the streaming pass (smp_stream.hip) has found each chunk's maximum, this kernel
+//   1. forms the row maximum M (sample.rs:377-379) and, for greedy rows, the argmax
+//      (sample.rs:369-371, 429-439);
+//   2. streams the row once more (from the caches, where the streaming pass left it) and
+//      computes the normalizer S = sum of exp(s - M) exactly as the reference's sequential
+//      f32 loop rounds it (sample.rs:381-386), by binade-quantized prefix sums with the
+//      rare events done as real f32 additions (smp_exact.h); on the way it gathers the
+//      candidates of the kept set (elements above a bound that top-k, top-p or min-p
+//      guarantees the kept set lies above) into LDS;
+//   3. gives each candidate its exact probability fl(expf(s - M) / S) and its reference
+//      order key (descending p, then ascending index: the stable sort of sample.rs:393,398);
+//   4. walks the candidates in that order by value buckets (a counting sort, no full sort):
+//      whole buckets are added as quantized sums, and only a bucket in which an event lies
+//      (a binade crossing, a tie, the top-p cut, the drawn position) is sorted and walked
+//      element by element. The walks give the top-p cut (sample.rs:397-409), the kept sum
+//      and the drawn token (sample.rs:312-323), or the judge's verdict and residual draw.
+// Rows without top-k / top-p draw in index order; without any filter they stream the row
+// twice more for the draw (sum, then the position).
+#include <hip/hip_ext.h>
+
+#define BFI_BLOCK 1024
+#include "smp_common.h"
+#include "smp_exact.h"
+
+namespace bfi {
+
+constexpr int LCAP = 8192;   // candidates held in LDS (beyond: the row's global spill area)
+constexpr int NB = 1024;     // value buckets of a walk
+constexpr int RNV_F32 = 2;   // 16-byte vectors per thread per step of a row stream (f32)
+constexpr int RNV_BF16 = 1;  // (bf16)
+
+struct __align__(16) RowSmem {
+    uint64_t list[LCAP];   // gathered candidates (id << 32 | bits(x)), then keys, then scratch
+    uint64_t grp[LCAP];    // the keys grouped by bucket
+    uint32_t bcnt[NB];     // per bucket: element count
+    uint32_t boff[NB];     // per bucket: first position in grp
+    uint32_t bfill[NB];    // per bucket: fill counter, then scratch
+    uint32_t wu[NWAVE];
+    uint32_t wu2[NWAVE];
+    float wf[NWAVE];
+    double wd[NWAVE];
+    uint64_t w64[NWAVE];
+    uint32_t misc[16];
+    float mf[16];
+};
+
+enum { MS_N = 0, MS_STOP = 1, MS_STOPLO = 2, MS_FLAG = 3, MS_TOK = 4, MS_VERDICT = 5, MS_KIND = 6, MS_LAST = 7 };
+enum { MF_S = 0, MF_CUM = 1 };
+
+// ---- row-wide history tables (global workspace) ---------------------------------------
+//
+// The reference's `HashSet(prev)` (sample.rs:347, 361) as a bitmap over the vocabulary,
+// plus the multiset counts of the frequency extension as dense counts over the set ids
+// (rank of an id = popcount prefix of the bitmap). Built once per row per launch.
+
+struct HistTabs {
+    const uint32_t* bm;
+    const uint32_t* pre;
+    const uint32_t* cnt;
+    bool dense;  // counts are in cnt (else, more than GDCAP distinct ids: scanned)
+};
+
+__device__ __noinline__ HistTabs build_hist_tabs(const KArgs& a, RowSmem& sm, const RowCtx& C) {
+    HistTabs T{nullptr, nullptr, nullptr, false};
+    if (!C.pen_on) return T;
+    const int tid = threadIdx.x;
+    const int nw = a.bm_words;
+    uint32_t* bm = a.row_pen + (int64_t)C.row * (2 * (int64_t)nw + GDCAP);
+    uint32_t* pre = bm + nw;
+    uint32_t* cnt = pre + nw;
+    for (int w = tid; w < nw; w += BLOCK) bm[w] = 0u;
+    if (C.pen.freq_on)
+        for (int w = tid; w < GDCAP; w += BLOCK) cnt[w] = 0u;
+    __threadfence();
+    __syncthreads();
+    const int64_t H = C.h.size();
+    for (int64_t j = tid; j < H; j += BLOCK) {
+        const uint32_t id = C.h.at(j);
+        if (id < (uint32_t)a.V) glb_or(&bm[id >> 5], 1u << (id & 31));
+    }
+    __threadfence();
+    __syncthreads();
+    bool dense = false;
+    if (C.pen.freq_on) {
+        const int per = (nw + BLOCK - 1) / BLOCK;
+        const int w0 = tid * per;
+        uint32_t s = 0;
+        for (int w = w0; w < w0 + per && w < nw; w++) s += __popc(bm[w]);
+        uint32_t tot;
+        uint32_t run = block_excl_scan<uint32_t>(s, sm.wu, tot);
+        for (int w = w0; w < w0 + per && w < nw; w++) {
+            pre[w] = run;
+            run += __popc(bm[w]);
+        }
+        dense = tot <= (uint32_t)GDCAP;
+        __threadfence();
+        __syncthreads();
+        if (dense) {
+            for (int64_t j = tid; j < H; j += BLOCK) {
+                const uint32_t id = C.h.at(j);
+                if (id < (uint32_t)a.V) glb_add(&cnt[dense_rank(pre[id >> 5], bm[id >> 5], id & 31)], 1u);
+            }
+        }
+        __threadfence();
+        __syncthreads();
+    }
+    T.bm = bm;
+    T.pre = pre;
+    T.cnt = cnt;
+    T.dense = dense;
+    return T;
+}
+
+// Occurrences of history id `id` (the frequency extension's count).
+__device__ __forceinline__ uint32_t hist_count(const HistTabs& T, const RowCtx& C, uint32_t id) {
+    if (!C.pen.freq_on) return 1u;
+    if (T.dense) return T.cnt[dense_rank(T.pre[id >> 5], T.bm[id >> 5], id & 31)];
+    return C.h.count_scan(id);
+}
+
+// The masked, penalized logit of element id (sample.rs:331-367) from its raw logit.
+__device__ __forceinline__ float pen_logit(const HistTabs& T, const RowCtx& C, uint32_t id, float l, bool allowed,
+                                           bool in_hist) {
+    float x = allowed ? l : -__builtin_inff();
+    if (in_hist) x = penalize(x, hist_count(T, C, id), C.pen);
+    return x;
+}
+
+// Raw logit of element id (one scalar or vector load).
+template <bool BF16>
+__device__ __forceinline__ float load_logit(const KArgs& a, int row, uint32_t id) {
+    if (BF16)
+        return __uint_as_float((uint32_t)((const uint16_t*)a.logits)[(int64_t)row * a.row_stride + id] << 16);
+    return ((const float*)a.logits)[(int64_t)row * a.row_stride + id];
+}
+template <bool BF16>
+__device__ __forceinline__ float elem_x(const KArgs& a, const HistTabs& T, const RowCtx& C, uint32_t id) {
+    const float l = load_logit<BF16>(a, C.row, id);
+    const bool allowed = !C.mrow || ((C.mrow[id >> 5] >> (id & 31)) & 1u);
+    const bool inh = C.pen_on && ((T.bm[id >> 5] >> (id & 31)) & 1u);
+    return pen_logit(T, C, id, l, allowed, inh);
+}
+
+// exp(s - M) of a penalized masked logit x, as the reference computes it (sample.rs:383):
+// s = x / T rounded (sample.rs:374), then expf of the rounded difference.
+__device__ __forceinline__ float exact_e(const RowCtx& C, float x, float M) {
+    if (!(x > -__builtin_inff())) return 0.0f;
+    const float s = div_T(x, C);
+    return expf_ref(s - M);
+}
+// fl(e / S), correctly rounded (a double quotient of two floats rounds to the float
+// quotient: 53 >= 2 * 24 + 2).
+__device__ __forceinline__ float exact_p(float e, float S) { return (float)((double)e / (double)S); }
+
+// ---- block helpers for 1024 threads ----------------------------------------------------
+
+__device__ __forceinline__ uint32_t wave_sum_sat(uint32_t v) {
+    return lane63(wave_scan_incl(v, 0u, [](uint32_t x, uint32_t y) { return sat_add(x, y); }));
+}
+__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t v) {
+    return wave_scan_incl(v, 0u, [](uint32_t x, uint32_t y) { return sat_add(x, y); });
+}
+// Saturating block sum and an OR of flags in one barrier pair.
+__device__ __forceinline__ uint32_t block_sum_sat_or(uint32_t v, uint32_t f, uint32_t& fo, RowSmem& sm) {
+    v = wave_sum_sat(v);
+    const uint32_t fw = __ballot(f != 0u) ? 1u : 0u;
+    if (lane_id() == 0) {
+        sm.wu[wave_id()] = v;
+        sm.wu2[wave_id()] = fw;
+    }
+    __syncthreads();
+    uint32_t r = 0, ro = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) {
+        r = sat_add(r, sm.wu[w]);
+        ro |= sm.wu2[w];
+    }
+    __syncthreads();
+    fo = ro;
+    return r;
+}
+// Exclusive saturating block scan (thread order); `total` receives the block sum.
+__device__ __forceinline__ uint32_t block_excl_scan_sat(uint32_t v, uint32_t& total, RowSmem& sm) {
+    const uint32_t x = wave_scan_sat(v);
+    if (lane_id() == WAVE - 1) sm.wu[wave_id()] = x;
+    __syncthreads();
+    uint32_t pre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) {
+        const uint32_t s = sm.wu[w];
+        if (w < wave_id()) pre = sat_add(pre, s);
+        tot = sat_add(tot, s);
+    }
+    __syncthreads();
+    total = tot;
+    // the in-wave exclusive prefix is the previous lane's inclusive one (a subtraction
+    // would be wrong once the sum saturates)
+    const uint32_t up = (uint32_t)__shfl_up((int)x, 1);
+    const uint32_t ex = lane_id() == 0 ? 0u : up;
+    return sat_add(pre, ex);
+}
+
+}  // namespace bfi
+
+namespace bfi {
+
+// ---- row streams: sequential f32 sums over the row in index order ------------------------
+//
+// A stream walks the row in index order and sums v_i from 0 exactly as the reference's
+// sequential f32 loop does: v_i = e_i = expf(s_i - M) (the normalizer, sample.rs:381-386) or
+// v_i = p_i = fl(e_i / S) (the draw over an unfiltered row, sample.rs:313-321). Per element
+// a hardware exp2 estimate of t = v / u (u = the spacing of the running sum's binade)
+// rounds to the exact unit count unless the estimate lies too close to a rounding
+// boundary; those few elements get the exact value (glibc expf, exact division). Options:
+// a threshold th (stop at the first i whose running sum reaches th: sample.rs:318), an
+// excluded index (spec.rs:89: the residual without the draft), and gathering of elements
+// whose d * log2(e) (d = s - M, estimated) is at least gth into the candidate list.
+
+struct StreamCfg {
+    int kind;      // 0: e, 1: p
+    float M;       // the row maximum of s = x / T
+    float S;       // kind 1: the normalizer
+    float th;      // threshold (+inf: none)
+    int64_t excl;  // excluded index (-1: none)
+    bool gather;
+    float gth;     // gather bound on d * log2(e)
+};
+struct StreamOut {
+    float cum;     // the sum at the stop (or over the whole row)
+    int64_t stop;  // the index where the running sum first reached th, or -1
+};
+
+// Per-state constants of the estimate t ~ 2^(x * log2(e)/T + K): K folds -M * log2(e), the
+// state's unit exponent and (kind 1) -log2(S). The estimate's exponent a differs from
+// log2 of the exact t by at most 2^-24 (6|a| + 6|Kc| + |K| + 5|ue| + 1.5) (the roundings of
+// 1/T, log2(e), the constants and the FMA, against the reference's roundings of x / T,
+// s - M and expf), so its relative error is below rho = 2^-24 (4.5|a| + 4.5|Kc| + |K| +
+// 3.6|ue| + 1.5) + 2^-18, the last term for the hardware exp2; kind 1 adds the division's
+// rounding and log2(S)'s error.
+struct StreamState {
+    uint32_t m;
+    int32_t ue;
+    float K, R0, gth;
+    uint32_t tu;  // threshold in units (0xFFFFFFFF: none)
+};
+__device__ __forceinline__ StreamState stream_state(float s, const StreamCfg& cfg, float Kc, float lS, float th) {
+    const SumState ss = sum_state(s);
+    StreamState st;
+    st.m = ss.m;
+    st.ue = ss.ue;
+    st.K = Kc - (float)ss.ue - (cfg.kind ? lS : 0.0f);
+    float r = (4.5f * fabsf(Kc) + fabsf(st.K) + 3.6f * fabsf((float)ss.ue) + 1.5f) * 0x1p-24f + 0x1p-18f;
+    if (cfg.kind) r += (6.0f * fabsf(lS) + 2.0f) * 0x1p-24f;
+    st.R0 = r;
+    st.gth = cfg.gth - (float)ss.ue;
+    st.tu = th < __builtin_inff() ? thresh_units(fmaxf(th, 0.0f), ss.ue) : 0xFFFFFFFFu;
+    return st;
+}
+
+// The exact value of element x (penalized masked logit).
+__device__ __forceinline__ float stream_exact(const RowCtx& C, const StreamCfg& cfg, float x) {
+    const float e = exact_e(C, x, cfg.M);
+    return cfg.kind ? exact_p(e, cfg.S) : e;
+}
+
+// Unit count of element x at the state, exact; tie: the element's rounding depends on the
+// running sum's parity (an event).
+__device__ __forceinline__ uint32_t stream_units(const RowCtx& C, const StreamCfg& cfg, const StreamState& st, float x,
+                                                 float& a_out, bool& tie) {
+    tie = false;
+    if (!(x > -__builtin_inff())) {  // masked: exp(-inf) = 0 exactly
+        a_out = -__builtin_inff();
+        return 0u;
+    }
+    const float a = __builtin_fmaf(x, C.rTl, st.K);
+    a_out = a;
+    const float ta = __builtin_amdgcn_exp2f(a);
+    const float q = __builtin_rintf(ta);
+    const float f = fabsf(ta - q);
+    const float rho = __builtin_fmaf(fabsf(a), 4.5f * 0x1p-24f, st.R0);
+    if (__builtin_fmaf(ta, rho, f) < 0.5f && ta < 8388608.0f) return (uint32_t)q;
+    const float t = units_of(stream_exact(C, cfg, x), st.ue);
+    tie = quant_tie(t);
+    return quant_units(t);
+}
+
+template <bool BF16, int NV>
+struct RawT {
+    uint4 w[NV];
+    uint32_t mw[NV];
+    uint32_t pw[NV];
+};
+
+template <bool BF16, int NV>
+__device__ __forceinline__ void row_load(const KArgs& a, const RowCtx& C, const HistTabs& T, uint32_t base,
+                                         RawT<BF16, NV>& r) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    typedef typename Elem<BF16>::T ET;
+    const ET* rp = (const ET*)a.logits + (int64_t)C.row * a.row_stride;
+    const uint32_t V = (uint32_t)a.V;
+    const uint32_t ninf = BF16 ? 0xFF80FF80u : 0xFF800000u;
+#pragma unroll
+    for (int q = 0; q < NV; q++) {
+        const uint32_t id0 = base + (uint32_t)(q * BLOCK + threadIdx.x) * EPV;
+        if (a.vec_ok && id0 + EPV <= V) {
+            r.w[q] = *(const uint4*)(rp + id0);
+        } else {
+            uint32_t ww[4] = {ninf, ninf, ninf, ninf};
+#pragma unroll
+            for (int e = 0; e < EPV; e++) {
+                if (id0 + e >= V) continue;
+                if (BF16) {
+                    const uint32_t b = (uint32_t)rp[id0 + e];
+                    ww[e >> 1] = (e & 1) ? (ww[e >> 1] & 0xFFFFu) | (b << 16) : (ww[e >> 1] & 0xFFFF0000u) | b;
+                } else {
+                    ww[e] = __float_as_uint((float)rp[id0 + e]);
+                }
+            }
+            r.w[q] = make_uint4(ww[0], ww[1], ww[2], ww[3]);
+        }
+        const uint32_t wi = id0 < V ? id0 >> 5 : 0u;
+        r.mw[q] = C.mrow ? C.mrow[wi] : 0xFFFFFFFFu;
+        r.pw[q] = C.pen_on ? T.bm[wi] : 0u;
+    }
+}
+
+// Masked, penalized logits of one vector.
+template <bool BF16, int NV>
+__device__ __forceinline__ void row_decode(const RowCtx& C, const HistTabs& T, const RawT<BF16, NV>& r, int q,
+                                           uint32_t id0, float (&x)[Elem<BF16>::EPV]) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    unpack16<BF16, NV>(r.w[q], x);
+    const uint32_t em = (1u << EPV) - 1u;
+    const uint32_t mb = (r.mw[q] >> (id0 & 31)) & em;
+    const uint32_t pb = (r.pw[q] >> (id0 & 31)) & em;
+#pragma unroll
+    for (int e = 0; e < EPV; e++) x[e] = ((mb >> e) & 1u) ? x[e] : -__builtin_inff();
+    if (pb) {
+#pragma unroll
+        for (int e = 0; e < EPV; e++)
+            if ((pb >> e) & 1u) x[e] = penalize(x[e], hist_count(T, C, id0 + e), C.pen);
+    }
+}
+
+// Appends (id, x) to the row's candidate list: LDS first, then the row's spill area.
+__device__ __forceinline__ void list_append(const KArgs& a, RowSmem& sm, const RowCtx& C, bool take, uint32_t id,
+                                            float x) {
+    const uint64_t bal = __ballot(take);
+    if (!bal) return;
+    const int leader = __ffsll((unsigned long long)bal) - 1;
+    uint32_t base = 0;
+    if (lane_id() == leader) base = lds_add(&sm.misc[MS_N], (uint32_t)__popcll(bal));
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
+    if (take) {
+        const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
+        const uint64_t ent = ((uint64_t)id << 32) | __float_as_uint(x);
+        if (pos < (uint32_t)LCAP) sm.list[pos] = ent;
+        else if (pos < (uint32_t)a.V) a.spill[(int64_t)C.row * 4 * a.V + pos] = ent;
+    }
+}
+
+template <bool BF16>
+__device__ __noinline__ StreamOut row_stream(const KArgs& a, RowSmem& sm, const RowCtx& C, const HistTabs& T,
+                                const StreamCfg& cfg) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    constexpr int NV = BF16 ? RNV_BF16 : RNV_F32;
+    constexpr uint32_t SPAN = (uint32_t)BLOCK * NV * EPV;
+    const int tid = threadIdx.x;
+    const uint32_t V = (uint32_t)a.V;
+    const float Kc = -(cfg.M * 1.44269504088896341f);
+    const float lS = cfg.kind ? __log2f(cfg.S) : 0.0f;
+    StreamState st = stream_state(0.0f, cfg, Kc, lS, cfg.th);
+    StreamOut out{0.0f, -1};
+    RawT<BF16, NV> ra, rb;
+    row_load<BF16, NV>(a, C, T, 0u, ra);
+    for (uint32_t base = 0; base < V; base += SPAN) {
+        // the next step's loads go out before this step is worked on
+        if (base + SPAN < V) row_load<BF16, NV>(a, C, T, base + SPAN, rb);
+        uint32_t qs = 0, tf = 0;
+#pragma unroll
+        for (int q = 0; q < NV; q++) {
+            const uint32_t id0 = base + (uint32_t)(q * BLOCK + tid) * EPV;
+            float xq[EPV];
+            row_decode<BF16, NV>(C, T, ra, q, id0, xq);
+#pragma unroll
+            for (int e = 0; e < EPV; e++) {
+                const uint32_t id = id0 + e;
+                float av;
+                bool tie;
+                uint32_t u = stream_units(C, cfg, st, xq[e], av, tie);
+                if ((int64_t)id == cfg.excl) {
+                    u = 0;
+                    tie = false;
+                }
+                qs = sat_add(qs, u);
+                tf |= tie ? 1u : 0u;
+                if (cfg.gather) list_append(a, sm, C, av >= st.gth && xq[e] > -__builtin_inff(), id, xq[e]);
+            }
+        }
+        uint32_t anytie;
+        const uint32_t tot = block_sum_sat_or(qs, tf, anytie, sm);
+        const uint32_t run = sat_add(st.m, tot);
+        if (!anytie && run < M_TOP && run < st.tu) {
+            st.m = run;
+        } else {
+            // an event in this step: vector by vector, element by element in index order
+#pragma unroll
+            for (int q = 0; q < NV; q++) {
+                const uint32_t id0 = base + (uint32_t)(q * BLOCK + tid) * EPV;
+                float xq[EPV];
+                row_decode<BF16, NV>(C, T, ra, q, id0, xq);
+                int done = -1;  // positions (thread * EPV + e) of this vector up to here are summed
+#pragma unroll 1
+                for (;;) {
+                    uint32_t lp[EPV];
+                    bool ev[EPV];
+                    uint32_t tt = 0;
+#pragma unroll
+                    for (int e = 0; e < EPV; e++) {
+                        const int pos = tid * EPV + e;
+                        float av;
+                        bool tie;
+                        uint32_t u = stream_units(C, cfg, st, xq[e], av, tie);
+                        if (pos <= done || (int64_t)(id0 + e) == cfg.excl) {
+                            u = 0;
+                            tie = false;
+                        }
+                        ev[e] = tie;
+                        tt = sat_add(tt, u);
+                        lp[e] = tt;
+                    }
+                    uint32_t vt;
+                    const uint32_t pre = block_excl_scan_sat(tt, vt, sm);
+                    uint32_t first = 0xFFFFFFFFu;
+#pragma unroll
+                    for (int e = EPV - 1; e >= 0; e--) {
+                        const uint32_t r = sat_add(st.m, sat_add(pre, lp[e]));
+                        if (ev[e] || r >= M_TOP || r >= st.tu) first = (uint32_t)(tid * EPV + e);
+                    }
+                    const uint32_t fw = wave_min_u(first);
+                    if (lane_id() == 0) sm.wu2[wave_id()] = fw;
+                    __syncthreads();
+                    uint32_t f = 0xFFFFFFFFu;
+#pragma unroll
+                    for (int w = 0; w < NWAVE; w++) f = min(f, sm.wu2[w]);
+                    if (f == 0xFFFFFFFFu) {
+                        __syncthreads();
+                        st.m = sat_add(st.m, vt);
+                        break;
+                    }
+                    if ((uint32_t)tid == f / EPV) {
+                        const int e = (int)(f % EPV);
+                        // the event element's values, selected without indexing registers
+                        uint32_t ex = 0u, lpe = 0u;
+                        bool eve = false;
+                        float xe = 0.0f;
+#pragma unroll
+                        for (int k = 0; k < EPV; k++) {
+                            if (k + 1 == e) ex = lp[k];
+                            if (k == e) {
+                                lpe = lp[k];
+                                eve = ev[k];
+                                xe = xq[k];
+                            }
+                        }
+                        const uint32_t rb4 = st.m + pre + ex;  // below 2^24: no event before
+                        const uint32_t ra4 = sat_add(st.m, sat_add(pre, lpe));
+                        float res;
+                        uint32_t stop = 0;
+                        if (!eve && ra4 < M_TOP) {
+                            res = state_value(ra4, st.ue);  // the threshold, inside the binade
+                            stop = 1;
+                        } else {
+                            const float sb = state_value(rb4, st.ue);
+                            const float v = stream_exact(C, cfg, xe);
+                            res = sb + v;  // the reference's own rounding of this step
+                            stop = res >= cfg.th ? 1u : 0u;
+                        }
+                        sm.mf[MF_S] = res;
+                        sm.misc[MS_STOP] = stop;
+                    }
+                    __syncthreads();
+                    const float sn = sm.mf[MF_S];
+                    const uint32_t stp = sm.misc[MS_STOP];
+                    __syncthreads();
+                    if (stp) {
+                        out.cum = sn;
+                        out.stop = (int64_t)(base + (uint32_t)q * BLOCK * EPV + f);
+                        return out;
+                    }
+                    st = stream_state(sn, cfg, Kc, lS, cfg.th);
+                    done = (int)f;
+                }
+            }
+        }
+        if (base + SPAN < V) ra = rb;
+    }
+    out.cum = state_value(st.m, st.ue);
+    return out;
+}
+
+}  // namespace bfi
+
+namespace bfi {
+
+// ---- the candidate list: exact keys, buckets, ordered walks ----------------------------
+//
+// Each gathered candidate gets its probability p = fl(expf(s - M) / S) and a key whose
+// descending order is the reference's: (ord(p) << 32 | ~id) for the sorted modes (stable
+// sort by descending p of an index-ordered list, sample.rs:393, 398), (~id << 32 | bits(p))
+// for the index-ordered min-p mode (retain keeps order, sample.rs:413). A counting sort puts
+// the keys into NB buckets by the key's high bits; within a bucket they stay unsorted.
+
+struct ListInfo {
+    const uint64_t* G;  // keys grouped by bucket (LDS or the row's spill area)
+    uint32_t n;         // keys in G (candidates with p >= p_safe, and for min-p p >= thresh)
+    uint32_t nb;        // buckets in use
+    uint64_t kmax;      // the largest key
+    int row;
+};
+
+__device__ __forceinline__ float key_p(uint64_t key, bool idxmode) {
+    return idxmode ? __uint_as_float((uint32_t)key) : __uint_as_float((uint32_t)(key >> 32) & 0x7FFFFFFFu);
+}
+__device__ __forceinline__ uint32_t key_id(uint64_t key, bool idxmode) {
+    return idxmode ? ~(uint32_t)(key >> 32) : ~(uint32_t)key;
+}
+__device__ __forceinline__ uint64_t make_key(float p, uint32_t id, bool idxmode) {
+    return idxmode ? (((uint64_t)(~id) << 32) | __float_as_uint(p))
+                   : (((uint64_t)(0x80000000u | __float_as_uint(p)) << 32) | (uint64_t)(~id));
+}
+
+__device__ __forceinline__ uint64_t* list_slot(const KArgs& a, RowSmem& sm, int row, uint32_t j) {
+    return j < (uint32_t)LCAP ? &sm.list[j] : &a.spill[(int64_t)row * 4 * a.V + j];
+}
+
+// Turns the gathered (id, x) entries into keys, keeps those with p >= p_lo (> 0), and groups
+// them by bucket. Every thread calls it.
+__device__ __noinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const RowCtx& C, float M, float S, float p_lo,
+                               bool idxmode) {
+    const int tid = threadIdx.x;
+    const uint32_t N = min(sm.misc[MS_N], (uint32_t)a.V);
+    uint32_t hmax = 0u, hmin = 0xFFFFFFFFu, nv = 0;
+    uint64_t kmax = 0;
+    for (uint32_t j = tid; j < N; j += BLOCK) {
+        uint64_t* sl = list_slot(a, sm, C.row, j);
+        const uint64_t ent = *sl;
+        const uint32_t id = (uint32_t)(ent >> 32);
+        const float p = exact_p(exact_e(C, __uint_as_float((uint32_t)ent), M), S);
+        uint64_t key = 0;
+        if (p > 0.0f && p >= p_lo) {
+            key = make_key(p, id, idxmode);
+            const uint32_t hi = (uint32_t)(key >> 32);
+            hmax = max(hmax, hi);
+            hmin = min(hmin, hi);
+            kmax = key > kmax ? key : kmax;
+            nv++;
+        }
+        *sl = key;
+    }
+    ListInfo L;
+    // reductions: max/min of the high words, the largest key, the count
+    {
+        const uint32_t wmx = lane63(wave_scan_incl(hmax, 0u, [](uint32_t x, uint32_t y) { return max(x, y); }));
+        const uint32_t wmn = wave_min_u(hmin);
+        const uint64_t wk = wave_max_u64(kmax);
+        const uint32_t wn = wave_sum_u(nv);
+        if (lane_id() == 0) {
+            sm.wu[wave_id()] = wmx;
+            sm.wu2[wave_id()] = wmn;
+            sm.w64[wave_id()] = wk;
+            sm.wf[wave_id()] = __uint_as_float(wn);
+        }
+        __syncthreads();
+        hmax = 0u;
+        hmin = 0xFFFFFFFFu;
+        kmax = 0;
+        nv = 0;
+#pragma unroll
+        for (int w = 0; w < NWAVE; w++) {
+            hmax = max(hmax, sm.wu[w]);
+            hmin = min(hmin, sm.wu2[w]);
+            kmax = sm.w64[w] > kmax ? sm.w64[w] : kmax;
+            nv += __float_as_uint(sm.wf[w]);
+        }
+        __syncthreads();
+    }
+    int sh = idxmode ? 0 : 18;
+    if (nv) while ((hmax >> sh) - (hmin >> sh) >= (uint32_t)NB) sh++;
+    const uint32_t top = hmax >> sh;
+    L.nb = nv ? top - (hmin >> sh) + 1 : 0;
+    L.n = nv;
+    L.kmax = kmax;
+    L.row = C.row;
+    uint64_t* G = nv <= (uint32_t)LCAP ? sm.grp : a.spill + (int64_t)C.row * 4 * a.V + a.V;
+    L.G = G;
+    for (int b = tid; b < NB; b += BLOCK) {
+        sm.bcnt[b] = 0u;
+        sm.bfill[b] = 0u;
+    }
+    __syncthreads();
+    for (uint32_t j = tid; j < N; j += BLOCK) {
+        const uint64_t key = *list_slot(a, sm, C.row, j);
+        if (key) lds_add(&sm.bcnt[top - ((uint32_t)(key >> 32) >> sh)], 1u);
+    }
+    __syncthreads();
+    {
+        uint32_t tot;
+        const uint32_t c = tid < NB ? sm.bcnt[tid] : 0u;
+        const uint32_t o = block_excl_scan<uint32_t>(c, sm.wu, tot);
+        if (tid < NB) sm.boff[tid] = o;
+    }
+    __syncthreads();
+    for (uint32_t j = tid; j < N; j += BLOCK) {
+        const uint64_t key = *list_slot(a, sm, C.row, j);
+        if (key) {
+            const uint32_t b = top - ((uint32_t)(key >> 32) >> sh);
+            G[sm.boff[b] + lds_add(&sm.bfill[b], 1u)] = key;
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
+    return L;
+}
+
+// Orders LDS writes of this wave before its later LDS reads (lanes of one wave only).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Bitonic sort (descending) of n keys at buf by one wave; n a power of two.
+__device__ __forceinline__ void wave_sort_lds(uint64_t* buf, int n) {
+    const int lane = lane_id();
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = lane; i < n / 2; i += WAVE) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool desc = (lo & size) == 0;
+                const uint64_t x = buf[lo], y = buf[hi];
+                if ((x < y) == desc) {
+                    buf[lo] = y;
+                    buf[hi] = x;
+                }
+            }
+            wave_lds_sync();
+        }
+    }
+}
+
+// The same in global memory (a bucket larger than LDS holds; the row's spill area), with a
+// device-scope fence between stages so the lanes see each other's stores.
+__device__ __forceinline__ void wave_sort_glb(uint64_t* buf, int n) {
+    const int lane = lane_id();
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = lane; i < n / 2; i += WAVE) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool desc = (lo & size) == 0;
+                const uint64_t x = __hip_atomic_load(&buf[lo], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t y = __hip_atomic_load(&buf[hi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((x < y) == desc) {
+                    __hip_atomic_store(&buf[lo], y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&buf[hi], x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            __threadfence();
+            __builtin_amdgcn_wave_barrier();
+            __threadfence();
+        }
+    }
+}
+
+// The n keys of a bucket (at src), sorted descending into a scratch buffer of n2 (a power of
+// two >= n) keys: LDS when they fit, else the row's spill area (its sort scratch).
+// Wave 0; returns the buffer.
+__device__ __forceinline__ uint64_t* sort_bucket(const KArgs& a, RowSmem& sm, int row, const uint64_t* src,
+                                                 uint32_t n, int n2) {
+    const int lane = lane_id();
+    uint64_t* buf = n2 <= LCAP ? sm.list : a.spill + (int64_t)row * 4 * a.V + 2 * (int64_t)a.V;
+    for (int j = lane; j < n2; j += WAVE) buf[j] = (uint32_t)j < n ? src[j] : 0ull;
+    if (n2 <= LCAP) {
+        wave_lds_sync();
+        wave_sort_lds(buf, n2);
+    } else {
+        __threadfence();
+        __builtin_amdgcn_wave_barrier();
+        wave_sort_glb(buf, n2);
+    }
+    return buf;
+}
+
+// A walk in key order from cum = 0: for each element (the excluded key adds nothing and has
+// no rank), cum = fl(cum + p). It stops at the first element where cum >= th (how 1) or at
+// the R-th element (how 2), else runs out (how 0) with the list's total.
+struct WalkOut {
+    float cum;
+    uint32_t rank;  // the stop element's rank (how 1, 2) or the element count (how 0)
+    uint64_t key;
+    int how;
+};
+
+struct WalkState {
+    uint32_t m;
+    int32_t ue;
+    uint32_t tu;
+    uint32_t r;
+};
+__device__ __forceinline__ void walk_set(WalkState& w, float s, float th) {
+    const SumState ss = sum_state(s);
+    w.m = ss.m;
+    w.ue = ss.ue;
+    w.tu = thresh_units(fmaxf(th, 0.0f), ss.ue);
+    if (!(th < __builtin_inff())) w.tu = 0xFFFFFFFFu;
+}
+
+// Element-level walk over one wave-load of sorted keys (one per lane, 0 = none). Returns
+// true when it stopped (o filled). Wave-uniform.
+__device__ __forceinline__ bool walk_elems(WalkState& w, uint64_t key, float th, uint32_t R, uint64_t excl,
+                                           bool idxmode, WalkOut& o) {
+    const int lane = lane_id();
+    int done = -1;
+    for (;;) {
+        const bool valid = key != 0 && key != excl && lane > done;
+        const float p = key_p(key, idxmode);
+        const float t = units_of(p, w.ue);
+        const uint32_t q = valid ? quant_units(t) : 0u;
+        const bool tie = valid && quant_tie(t);
+        const uint32_t c = valid ? 1u : 0u;
+        const uint32_t Qi = wave_scan_sat(q);
+        const uint32_t Ci = wave_scan_incl(c, 0u, [](uint32_t x, uint32_t y) { return x + y; });
+        const uint32_t run = sat_add(w.m, Qi);
+        const bool ev = valid && (tie || run >= M_TOP || run >= w.tu || (uint64_t)w.r + Ci >= (uint64_t)R);
+        const uint64_t bal = __ballot(ev);
+        if (!bal) {
+            w.m = lane63(run);
+            w.r += lane63(Ci);
+            return false;
+        }
+        const int j = __ffsll((unsigned long long)bal) - 1;
+        const uint32_t run_j = (uint32_t)__builtin_amdgcn_readlane((int)run, j);
+        const uint32_t runb = j ? (uint32_t)__builtin_amdgcn_readlane((int)run, j - 1) : w.m;
+        const uint32_t ci_j = (uint32_t)__builtin_amdgcn_readlane((int)Ci, j);
+        const bool tie_j = __builtin_amdgcn_readlane((int)tie, j) != 0;
+        const uint64_t key_j = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), j) << 32) |
+                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, j);
+        const uint32_t rank_j = w.r + ci_j - 1;
+        if (!tie_j && run_j < M_TOP) {
+            o.cum = state_value(run_j, w.ue);
+            o.rank = rank_j;
+            o.key = key_j;
+            o.how = run_j >= w.tu ? 1 : 2;
+            return true;
+        }
+        const float sn = state_value(runb, w.ue) + key_p(key_j, idxmode);
+        if (sn >= th || (uint64_t)w.r + ci_j >= (uint64_t)R) {
+            o.cum = sn;
+            o.rank = rank_j;
+            o.key = key_j;
+            o.how = sn >= th ? 1 : 2;
+            return true;
+        }
+        walk_set(w, sn, th);
+        w.r = rank_j + 1;
+        done = j;
+    }
+}
+
+// The walk, done by wave 0 (the result is broadcast through LDS to every thread).
+__device__ __noinline__ WalkOut walk(const KArgs& a, RowSmem& sm, const ListInfo& L, float th, uint32_t R, uint64_t excl, bool idxmode) {
+    WalkOut o{0.0f, 0u, 0ull, 0};
+    if (wave_id() == 0) {
+        const int lane = lane_id();
+        WalkState w;
+        walk_set(w, 0.0f, th);
+        w.r = 0;
+        bool stopped = false;
+        uint32_t b0 = 0;
+        while (b0 < L.nb && !stopped) {
+            const uint32_t b = b0 + (uint32_t)lane;
+            const uint32_t cnt = b < L.nb ? sm.bcnt[b] : 0u;
+            const uint32_t off = b < L.nb ? sm.boff[b] : 0u;
+            uint32_t Q = 0, c = 0;
+            bool tie = false;
+            for (uint32_t j = 0; j < cnt; j++) {
+                const uint64_t key = L.G[off + j];
+                if (key == excl) continue;
+                const float t = units_of(key_p(key, idxmode), w.ue);
+                Q = sat_add(Q, quant_units(t));
+                tie = tie || quant_tie(t);
+                c++;
+            }
+            const uint32_t Qi = wave_scan_sat(Q);
+            const uint32_t Ci = wave_scan_incl(c, 0u, [](uint32_t x, uint32_t y) { return x + y; });
+            const uint32_t run = sat_add(w.m, Qi);
+            const bool ev = c > 0 && (tie || run >= M_TOP || run >= w.tu || (uint64_t)w.r + Ci >= (uint64_t)R);
+            const uint64_t bal = __ballot(ev);
+            if (!bal) {
+                w.m = lane63(run);
+                w.r += lane63(Ci);
+                b0 += WAVE;
+                continue;
+            }
+            const int s = __ffsll((unsigned long long)bal) - 1;
+            if (s > 0) {
+                w.m = (uint32_t)__builtin_amdgcn_readlane((int)run, s - 1);
+                w.r += (uint32_t)__builtin_amdgcn_readlane((int)Ci, s - 1);
+            }
+            // the bucket of the event, sorted and walked element by element
+            const uint32_t bs = b0 + (uint32_t)s;
+            const uint32_t n = sm.bcnt[bs], o0 = sm.boff[bs];
+            if (n <= (uint32_t)WAVE) {
+                uint64_t key = (uint32_t)lane < n ? L.G[o0 + lane] : 0ull;
+                key = wave_sort_desc(key);
+                stopped = walk_elems(w, key, th, R, excl, idxmode, o);
+            } else {
+                int n2 = WAVE;
+                while ((uint32_t)n2 < n) n2 <<= 1;
+                const uint64_t* buf = sort_bucket(a, sm, L.row, L.G + o0, n, n2);
+                for (int j0 = 0; j0 < (int)n && !stopped; j0 += WAVE)
+                    stopped = walk_elems(w, buf[j0 + lane], th, R, excl, idxmode, o);
+            }
+            b0 = bs + 1;
+        }
+        if (!stopped) {
+            o.cum = state_value(w.m, w.ue);
+            o.rank = w.r;
+            o.key = 0;
+            o.how = 0;
+        }
+        if (lane == 0) {
+            sm.mf[MF_CUM] = o.cum;
+            sm.misc[MS_STOP] = o.rank;
+            sm.misc[MS_STOPLO] = (uint32_t)o.key;
+            sm.misc[MS_FLAG] = (uint32_t)(o.key >> 32);
+            sm.misc[MS_KIND] = (uint32_t)o.how;
+        }
+    }
+    __syncthreads();
+    o.cum = sm.mf[MF_CUM];
+    o.rank = sm.misc[MS_STOP];
+    o.key = ((uint64_t)sm.misc[MS_FLAG] << 32) | sm.misc[MS_STOPLO];
+    o.how = (int)sm.misc[MS_KIND];
+    __syncthreads();
+    return o;
+}
+
+// Lists the first `lim` keys in order (ids and probabilities) into the row's target
+// arrays (target_rows' kept list). Wave 0.
+__device__ __noinline__ void list_kept(const KArgs& a, RowSmem& sm, const ListInfo& L, int row, uint32_t lim, bool idxmode) {
+    if (wave_id() == 0) {
+        const int lane = lane_id();
+        uint32_t w = 0;
+        for (uint32_t b = 0; b < L.nb && w < lim; b++) {
+            const uint32_t n = sm.bcnt[b], o0 = sm.boff[b];
+            if (!n) continue;
+            int n2 = WAVE;
+            while ((uint32_t)n2 < n) n2 <<= 1;
+            const uint64_t* buf = sort_bucket(a, sm, row, L.G + o0, n, n2);
+            for (uint32_t j = lane; j < n; j += WAVE) {
+                const uint32_t pos = w + j;
+                if (pos < lim) {
+                    const uint64_t key = buf[j];
+                    a.t_ids[(int64_t)row * a.t_cap + pos] = key_id(key, idxmode);
+                    a.t_probs[(int64_t)row * a.t_cap + pos] = key_p(key, idxmode);
+                }
+            }
+            w += n;
+            wave_lds_sync();
+        }
+    }
+    __syncthreads();
+}
+
+}  // namespace bfi
+
+namespace bfi {
+
+// ---- results -----------------------------------------------------------------------------
+
+// Stores the row's outcome. For spec verify, `verdict` is 1 = Accept, 0 = Reject(token);
+// the last row of a sequence to finish resolves the accepted prefix (spec.rs:140-162).
+__device__ void row_emit(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t token, uint32_t verdict) {
+    const int tid = threadIdx.x;
+    if (!C.verify) {
+        if (tid == 0 && a.out_tok) a.out_tok[C.row] = token;
+        return;
+    }
+    if (tid == 0) {
+        a.row_res[2 * C.row] = C.judged ? verdict : 2u;
+        a.row_res[2 * C.row + 1] = token;
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = glb_add(&a.seq_ctr[C.seq], 1u);
+        sm.misc[MS_LAST] = prev == (uint32_t)C.dl;
+    }
+    __syncthreads();
+    if (!sm.misc[MS_LAST]) return;
+    __threadfence();
+    if (tid == 0) {
+        a.seq_ctr[C.seq] = 0;
+        const int base = C.seq * a.rows_per_seq;
+        int acc = C.dl;
+        for (int i = 0; i < C.dl; i++) {
+            if (__hip_atomic_load(&a.row_res[2 * (base + i)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+                acc = i;
+                break;
+            }
+        }
+        a.out_accepted[C.seq] = acc;
+        a.out_next[C.seq] =
+            __hip_atomic_load(&a.row_res[2 * (base + acc) + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// A token target (greedy, min-p fallback): judge is equality (spec.rs:81-82).
+__device__ void finish_token(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t tok) {
+    if (threadIdx.x == 0 && a.t_kind) {
+        a.t_kind[C.row] = BFI_SMP_TARGET_TOKEN;
+        a.t_kept[C.row] = 0;
+        a.t_listed[C.row] = 0;
+    }
+    row_emit(a, sm, C, tok, C.judged ? (tok == C.draft ? 1u : 0u) : 1u);
+}
+
+__device__ void target_weights(const KArgs& a, const RowCtx& C, int64_t L, int64_t listed) {
+    if (threadIdx.x == 0 && a.t_kind) {
+        a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
+        a.t_kept[C.row] = (int32_t)min(L, (int64_t)INT32_MAX);
+        a.t_listed[C.row] = (int32_t)listed;
+    }
+}
+
+__device__ void put_stats(const KArgs& a, const RowCtx& C, float M, float S, float kept, float mode) {
+    if (threadIdx.x == 0 && a.t_stats) {
+        a.t_stats[C.row * 4 + 0] = M;
+        a.t_stats[C.row * 4 + 1] = S;
+        a.t_stats[C.row * 4 + 2] = kept;
+        a.t_stats[C.row * 4 + 3] = mode;
+    }
+}
+
+// ---- row maximum over the penalized values (histories the streaming pass left out) -------
+
+template <bool BF16>
+__device__ __noinline__ ArgMax row_max(const KArgs& a, RowSmem& sm, const RowCtx& C, const HistTabs& T) {
+    constexpr int EPV = Elem<BF16>::EPV;
+    constexpr int NV = BF16 ? RNV_BF16 : RNV_F32;
+    constexpr uint32_t SPAN = (uint32_t)BLOCK * NV * EPV;
+    const uint32_t V = (uint32_t)a.V;
+    ArgMax best{-__builtin_inff(), 0xFFFFFFFFu};
+    for (uint32_t base = 0; base < V; base += SPAN) {
+        RawT<BF16, NV> r;
+        row_load<BF16, NV>(a, C, T, base, r);
+#pragma unroll
+        for (int q = 0; q < NV; q++) {
+            const uint32_t id0 = base + (uint32_t)(q * BLOCK + threadIdx.x) * EPV;
+            float x[EPV];
+            row_decode<BF16, NV>(C, T, r, q, id0, x);
+#pragma unroll
+            for (int e = 0; e < EPV; e++)
+                if (id0 + e < V) best = argmax_merge(best, ArgMax{x[e], id0 + e});
+        }
+    }
+    return block_argmax(best, sm.wf, sm.wu);
+}
+
+// ---- the gather bound from the streaming pass's histograms ------------------------------
+//
+// Bin j of chunk c holds the elements j/8 .. (j+1)/8 log2-units below the chunk maximum
+// xm_c, which lies o_c = (xmax - xm_c) log2(e)/T below the row's. On a grid of bounds
+// theta_g = -g/8 (in log2-units of exp(s - M)) this gives lower bounds on the count and on
+// the mass exp(s - M) of the elements above theta_g (bins entirely above it). The bound is
+// the highest theta_g whose lower bound reaches k (top-k) or the top-p mass with margins
+// for the reference's rounding (sample.rs:397-409); every kept element lies above it.
+constexpr int NGRID = 512;
+constexpr double MFIX = 1099511627776.0;  // 2^40: fixed point of the grid masses
+
+__device__ __noinline__ float gather_bound(const KArgs& a, RowSmem& sm, const RowCtx& C, float xmax) {
+    const int tid = threadIdx.x;
+    const int nc = a.n_chunks;
+    uint32_t* CL = sm.bcnt;
+    uint64_t* ML = sm.grp;
+    for (int g = tid; g < NGRID; g += BLOCK) {
+        CL[g] = 0u;
+        ML[g] = 0ull;
+    }
+    __syncthreads();
+    double sapprox = 0.0;
+    const float eps = 0x1p-8f;
+    for (int idx = tid; idx < nc * HBINS; idx += BLOCK) {
+        const int c = idx / HBINS, j = idx % HBINS;
+        const ChunkPart& P = a.parts[(int64_t)C.row * nc + c];
+        const float xm = P.xm;
+        if (!(xm > -__builtin_inff())) continue;
+        const float o = (xmax - xm) * C.rTl;
+        if (j == 0) sapprox += P.sum * exp2((double)-o);
+        const uint32_t cnt = a.vhist[((int64_t)C.row * nc + c) * HBINS + j];
+        if (!cnt || j == HBINS - 1) continue;
+        const float glo = ceilf(8.0f * o + (float)(j + 1) + 8.0f * eps);
+        if (glo < (float)NGRID) {
+            const int g = (int)glo;
+            lds_add(&CL[g], cnt);
+            const double m = (double)cnt * exp2(-(double)o - (double)(j + 1) / 8.0 - (double)eps);
+            lds_add64(&ML[g], (uint64_t)(m * MFIX));
+        }
+    }
+    const double S_hi = block_sum_d(sapprox, sm.wd) * (1.0 + 1e-4);
+    __syncthreads();
+    // inclusive prefixes over the grid
+    uint32_t cl = tid < NGRID ? CL[tid] : 0u;
+    uint64_t ml = tid < NGRID ? ML[tid] : 0ull;
+    uint32_t ct;
+    uint64_t mt;
+    cl += block_excl_scan<uint32_t>(cl, sm.wu, ct);
+    ml += block_excl_scan<uint64_t>(ml, sm.w64, mt);
+    uint32_t gk = 0xFFFFFFFFu, gp = 0xFFFFFFFFu;
+    if (tid < NGRID) {
+        if (C.kmode && cl >= (uint32_t)C.k) gk = (uint32_t)tid;
+        const double tgt = (double)min(C.top_p * 1.01f + 3e-4f, 2.0f) * S_hi * MFIX;
+        if (C.pmode && (double)ml >= tgt) gp = (uint32_t)tid;
+    }
+    gk = block_min_u(gk, sm.wu);
+    gp = block_min_u(gp, sm.wu);
+    float th = -__builtin_inff();
+    if (C.kmode && gk != 0xFFFFFFFFu) th = fmaxf(th, -(float)gk / 8.0f);
+    if (C.pmode && gp != 0xFFFFFFFFu) th = fmaxf(th, -(float)gp / 8.0f);
+    return th;
+}
+
+// ---- the row kernel ----------------------------------------------------------------------
+
+constexpr uint32_t LINF = 0xFFFFFFFFu;
+
+template <bool BF16>
+__device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
+    const int tid = threadIdx.x;
+    const RowCtx C = make_ctx(a, row);
+    if (!C.active) return;  // a verify row past its draft
+    const int nc = a.n_chunks;
+    const uint32_t V = (uint32_t)a.V;
+    // 1. chunk results: the row maximum, argmax keys
+    float M = -__builtin_inff(), xmax = -__builtin_inff();
+    uint64_t gk = 0, rk = 0;
+    for (int c = tid; c < nc; c += BLOCK) {
+        const ChunkPart P = a.parts[(int64_t)row * nc + c];
+        M = fmaxf(M, P.m);
+        xmax = fmaxf(xmax, P.xm);
+        if (C.greedy) {
+            const uint64_t k = argmax_key(P.m, P.arg);
+            gk = k > gk ? k : gk;
+        }
+        if (C.min_p > 1.0f) {
+            const uint64_t k = argmax_key(P.raw_m, P.raw_arg);
+            rk = k > rk ? k : rk;
+        }
+    }
+    M = block_max(M, sm.wf);
+    xmax = block_max(xmax, sm.wf);
+    gk = block_max_u64(gk, sm.w64);
+    rk = block_max_u64(rk, sm.w64);
+    const uint32_t raw_tok = rk ? argmax_of_key(rk).i : 0u;  // min-p fallback (sample.rs:415-422)
+    const HistTabs T = build_hist_tabs(a, sm, C);
+    if (C.pen_hash) {  // the streaming pass left the penalties out: the maximum again
+        const ArgMax am = row_max<BF16>(a, sm, C, T);
+        xmax = am.v;
+        M = C.greedy ? am.v : div_T(am.v, C);
+        gk = argmax_key(am.v, am.i);
+    }
+    if (C.greedy) {  // sample.rs:369-371
+        const ArgMax am = argmax_of_key(gk);
+        finish_token(a, sm, C, am.v > -__builtin_inff() ? am.i : 0u);
+        return;
+    }
+    const uint32_t Lk = C.kmode ? (uint32_t)C.k : V;
+    if (!(M > -__builtin_inff())) {
+        // every logit masked: exp(-inf - -inf) is NaN for all, so no cut applies, min-p keeps
+        // nothing (argmax of -infs = 0), and the draw's `r <= cum` never holds: last id.
+        put_stats(a, C, M, __builtin_nanf(""), __builtin_nanf(""), 0.0f);
+        if (C.mmode) {
+            finish_token(a, sm, C, 0u);
+            return;
+        }
+        target_weights(a, C, Lk, 0);
+        if (!C.judged) {
+            row_emit(a, sm, C, Lk - 1, 1u);
+        } else {
+            const bool dk = C.draft < Lk;
+            const uint32_t nres = Lk - (dk ? 1u : 0u);
+            if (nres == 0) row_emit(a, sm, C, C.draft, 1u);
+            else row_emit(a, sm, C, (dk && C.draft == Lk - 1) ? Lk - 2 : Lk - 1, 0u);
+        }
+        return;
+    }
+    // 2. the gather bound (log2-units below the maximum)
+    const bool sorted = C.kmode || C.pmode;
+    float th = -__builtin_inff();
+    if (sorted && !C.pen_hash && a.vhist) th = gather_bound(a, sm, C, xmax);
+    if (C.mmode) th = fmaxf(th, log2f(C.min_p) - 0x1p-6f);
+    const bool list_mode = sorted || C.mmode;
+    // 3. the normalizer, gathering the candidates on the way
+    if (tid == 0) sm.misc[MS_N] = 0u;
+    __syncthreads();
+    StreamCfg cfg{0, M, 0.0f, __builtin_inff(), -1, list_mode, th - 0x1p-8f};
+    const float S = row_stream<BF16>(a, sm, C, T, cfg).cum;  // sample.rs:381-386
+    __syncthreads();
+    bool exhaustive = !(th > -__builtin_inff());
+    const float p1 = exact_p(1.0f, S);  // the largest probability (the maximum's e is 1)
+    if (sorted) {
+        for (int attempt = 0; attempt < 2; attempt++) {
+            const float p_lo = exhaustive ? 0.0f : (float)(exp2((double)th) / (double)S * (1.0 + 0x1p-20));
+            const ListInfo L = build_list(a, sm, C, M, S, p_lo, false);
+            // top-p (sample.rs:397-409)
+            uint32_t Lp = Lk;
+            WalkOut o1{0.0f, 0u, 0ull, 0};
+            if (C.pmode) {
+                o1 = walk(a, sm, L, C.top_p, Lk, 0ull, false);
+                if (o1.how == 1) Lp = o1.rank + 1;
+                else if (o1.how == 0 && !exhaustive) Lp = LINF;
+            }
+            // min-p (sample.rs:411-424): thresh = min_p * max p, kept: p >= thresh
+            uint32_t Lm = Lp;
+            if (C.mmode) {
+                const float thresh = C.min_p * key_p(L.kmax, false);
+                if (thresh > 0.0f) {
+                    uint32_t cnt = 0;
+                    for (uint32_t j = tid; j < L.n; j += BLOCK) cnt += key_p(L.G[j], false) >= thresh ? 1u : 0u;
+                    cnt = block_sum_u(cnt, sm.wu);
+                    Lm = min(Lp, cnt);
+                }
+            }
+            const uint32_t Lfin = min(Lp, Lm);
+            if (C.mmode && Lfin == 0) {
+                put_stats(a, C, M, S, 0.0f, 2.0f);
+                finish_token(a, sm, C, raw_tok);
+                return;
+            }
+            if (Lfin == LINF || (Lfin > L.n && !exhaustive)) {  // the list does not reach the cut
+                exhaustive = true;
+                if (tid == 0) sm.misc[MS_N] = 0u;
+                __syncthreads();
+                StreamCfg all{0, M, 0.0f, __builtin_inff(), -1, true, -__builtin_inff()};
+                (void)row_stream<BF16>(a, sm, C, T, all);
+                __syncthreads();
+                continue;
+            }
+            const uint32_t npos = min(Lfin, L.n);  // kept elements with p > 0
+            // the kept sum (sample.rs:313)
+            float sum;
+            uint64_t klast;
+            if (C.pmode && o1.how == 1 && Lfin == Lp) {
+                sum = o1.cum;
+                klast = o1.key;
+            } else {
+                const WalkOut o2 = walk(a, sm, L, __builtin_inff(), Lfin, 0ull, false);
+                sum = o2.cum;
+                klast = o2.how == 2 ? o2.key : 0ull;
+            }
+            put_stats(a, C, M, S, sum, 1.0f);
+            if (!C.judged) {  // draw (sample.rs:312-323)
+                const float r = C.u * fmaxf(sum, 0.0f);
+                const WalkOut o3 = walk(a, sm, L, r, Lfin, 0ull, false);
+                const uint32_t tok = o3.how ? key_id(o3.key, false) : 0u;
+                if (a.t_kind) {
+                    const uint32_t lim = (uint32_t)min((int64_t)npos, a.t_cap);
+                    target_weights(a, C, Lfin, lim);
+                    if (lim) list_kept(a, sm, L, row, lim, false);
+                }
+                row_emit(a, sm, C, tok, 1u);
+                return;
+            }
+            // judge (spec.rs:83-95)
+            const uint32_t d = C.draft;
+            float pd = 0.0f;
+            if (d < V) pd = exact_p(exact_e(C, elem_x<BF16>(a, T, C, d), M), S);
+            const uint64_t kd = make_key(pd, d, false);
+            const bool dk = pd > 0.0f && (klast == 0ull || kd >= klast);
+            const float pdk = dk ? pd : 0.0f;
+            if (sum > 0.0f && C.u < exact_p(pdk, sum)) {
+                row_emit(a, sm, C, d, 1u);
+                return;
+            }
+            if (npos - (dk ? 1u : 0u) == 0u) {  // the residual has no positive weight
+                row_emit(a, sm, C, d, 1u);
+                return;
+            }
+            const uint64_t ex = dk ? kd : 0ull;
+            const uint32_t Lr = Lfin - (dk ? 1u : 0u);
+            const WalkOut o4 = walk(a, sm, L, __builtin_inff(), Lr, ex, false);
+            const float r2 = C.u2 * fmaxf(o4.cum, 0.0f);
+            const WalkOut o5 = walk(a, sm, L, r2, Lr, ex, false);
+            row_emit(a, sm, C, o5.how ? key_id(o5.key, false) : 0u, 0u);
+            return;
+        }
+        return;  // not reached: the second attempt gathers every element
+    }
+    const float thresh = C.mmode ? C.min_p * p1 : 0.0f;
+    if (C.mmode && thresh > 0.0f) {
+        // min-p alone: the kept elements in index order (sample.rs:411-414)
+        const ListInfo L = build_list(a, sm, C, M, S, thresh, true);
+        if (L.n == 0) {
+            put_stats(a, C, M, S, 0.0f, 2.0f);
+            finish_token(a, sm, C, raw_tok);
+            return;
+        }
+        const WalkOut o2 = walk(a, sm, L, __builtin_inff(), L.n, 0ull, true);
+        const float sum = o2.cum;
+        put_stats(a, C, M, S, sum, 3.0f);
+        if (!C.judged) {
+            const float r = C.u * fmaxf(sum, 0.0f);
+            const WalkOut o3 = walk(a, sm, L, r, L.n, 0ull, true);
+            if (a.t_kind) {
+                const uint32_t lim = (uint32_t)min((int64_t)L.n, a.t_cap);
+                target_weights(a, C, L.n, lim);
+                if (lim) list_kept(a, sm, L, row, lim, true);
+            }
+            row_emit(a, sm, C, o3.how ? key_id(o3.key, true) : 0u, 1u);
+            return;
+        }
+        const uint32_t d = C.draft;
+        float pd = 0.0f;
+        if (d < V) pd = exact_p(exact_e(C, elem_x<BF16>(a, T, C, d), M), S);
+        const bool dk = pd >= thresh && pd > 0.0f;
+        const float pdk = dk ? pd : 0.0f;
+        if (sum > 0.0f && C.u < exact_p(pdk, sum)) {
+            row_emit(a, sm, C, d, 1u);
+            return;
+        }
+        if (L.n - (dk ? 1u : 0u) == 0u) {
+            row_emit(a, sm, C, d, 1u);
+            return;
+        }
+        const uint64_t ex = dk ? make_key(pd, d, true) : 0ull;
+        const uint32_t Lr = L.n - (dk ? 1u : 0u);
+        const WalkOut o4 = walk(a, sm, L, __builtin_inff(), Lr, ex, true);
+        const float r2 = C.u2 * fmaxf(o4.cum, 0.0f);
+        const WalkOut o5 = walk(a, sm, L, r2, Lr, ex, true);
+        row_emit(a, sm, C, o5.how ? key_id(o5.key, true) : 0u, 0u);
+        return;
+    }
+    // no filter: the whole row in index order (sample.rs:312-323 over every element)
+    StreamCfg pc{1, M, S, __builtin_inff(), -1, false, 0.0f};
+    const float sum = row_stream<BF16>(a, sm, C, T, pc).cum;
+    put_stats(a, C, M, S, sum, 4.0f);
+    if (!C.judged) {
+        StreamCfg dc = pc;
+        dc.th = C.u * fmaxf(sum, 0.0f);
+        const StreamOut so = row_stream<BF16>(a, sm, C, T, dc);
+        const uint32_t tok = so.stop >= 0 ? (uint32_t)so.stop : V - 1u;
+        if (a.t_kind) {
+            // the positive entries in index order, up to the cap
+            uint32_t listed = 0;
+            for (uint32_t b0 = 0; b0 < V; b0 += BLOCK) {
+                const uint32_t id = b0 + (uint32_t)tid;
+                float p = 0.0f;
+                if (id < V) p = exact_p(exact_e(C, elem_x<BF16>(a, T, C, id), M), S);
+                const bool pos = p > 0.0f;
+                uint32_t tot;
+                const uint32_t o = block_excl_scan<uint32_t>(pos ? 1u : 0u, sm.wu, tot);
+                if (pos && (int64_t)(listed + o) < a.t_cap) {
+                    a.t_ids[(int64_t)row * a.t_cap + listed + o] = id;
+                    a.t_probs[(int64_t)row * a.t_cap + listed + o] = p;
+                }
+                listed += tot;
+            }
+            target_weights(a, C, V, min((int64_t)listed, a.t_cap));
+        }
+        row_emit(a, sm, C, tok, 1u);
+        return;
+    }
+    const uint32_t d = C.draft;
+    float pd = 0.0f;
+    if (d < V) pd = exact_p(exact_e(C, elem_x<BF16>(a, T, C, d), M), S);
+    if (sum > 0.0f && C.u < exact_p(pd, sum)) {
+        row_emit(a, sm, C, d, 1u);
+        return;
+    }
+    StreamCfg rc = pc;
+    rc.excl = d < V ? (int64_t)d : -1;
+    const float sres = row_stream<BF16>(a, sm, C, T, rc).cum;
+    if (!(sres > 0.0f)) {  // empty residual, or all of its weights 0
+        row_emit(a, sm, C, d, 1u);
+        return;
+    }
+    rc.th = C.u2 * sres;
+    const StreamOut so = row_stream<BF16>(a, sm, C, T, rc);
+    const uint32_t last = (d == V - 1u) ? V - 2u : V - 1u;
+    row_emit(a, sm, C, so.stop >= 0 ? (uint32_t)so.stop : last, 0u);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(BLOCK) void k_row(KArgs a) {
+    __shared__ RowSmem sm;
+    row_main<BF16>(a, sm, (int)blockIdx.x);
+}
+
+hipError_t launch_row(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+    const dim3 grid((unsigned)a.n_rows), block(BLOCK);
+    if (bf16) hipExtLaunchKernelGGL((k_row<true>), grid, block, 0, stream, start, stop, 0, a);
+    else hipExtLaunchKernelGGL((k_row<false>), grid, block, 0, stream, start, stop, 0, a);
+    return hipGetLastError();
+}
+
+}  // namespace bfi

@@ -3,96 +3,35 @@
 // One launch covers every row of a batch (generate_batch's per-step call, engine/mod.rs:
 // 316-322) or every draft row of a spec-verify step (engine/spec.rs:137-162). Workgroup
 // (row, chunk) reads `chunk` logits of one row once from HBM with 16-byte loads, keeps them
-// in VGPRs, applies the allow-mask and the temperature division (sample.rs:331-337,
-// 373-375), and writes per chunk: the max, the f64 sum of exp(s - max), and the elements
-// that can still be kept under the row's top-k or min-p bound. Penalties are left to the
-// select kernel, which corrects the few history ids.
+// in VGPRs and applies the allow-mask (sample.rs:331-337) and, for histories of at most
+// PREPEN_H ids, the penalties (sample.rs:345-367). Per chunk it writes the exact maximum of
+// x / T (sample.rs:373-379), the first index of the maximum for greedy rows (sample.rs:
+// 429-439) and of the un-penalized maximum for the min-p fallback (sample.rs:415-422), an
+// approximate f64 mass, and for top-k / top-p rows a 128-bucket histogram of how far below
+// the chunk maximum its elements lie. The row kernel (smp_row.hip) takes it from there.
 #include <hip/hip_ext.h>
 
 #include "smp_common.h"
 
 namespace bfi {
 
-// The stream kernel needs only reduction scratch (no history: penalties are applied as
-// sparse corrections by the select kernel). Each exchange has slots of its own, so one
-// barrier per exchange suffices.
-constexpr int SEG = 512;  // candidates one wave stages in LDS
 struct __align__(16) StreamSmem {
     double ws[NWAVE];   // per-wave sums (relative to the wave max)
     float wm[NWAVE];    // per-wave maxima of the masked logits
     float wbv[NWAVE];   // per-wave argmax value (greedy rows: penalized; min_p > 1: raw)
     uint32_t wa[NWAVE]; // per-wave first index of that value
-    uint32_t wc[NWAVE]; // per-wave candidate counts
-    uint32_t wc2[NWAVE];
-    float rf[NWAVE];
-    uint32_t ru[NWAVE];
-    double rd[NWAVE];
-    union {
-        uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids, two 16-bit halves a word
-        Cand stage[NWAVE][SEG];      // each wave's candidates before the coalesced copy out
-    } u;
+    uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids, two 16-bit halves a word;
+                                 // then the histogram (HBINS words)
 };
-static_assert(NWAVE * SEG * sizeof(Cand) == CHUNK_MAX * 2, "the count array and the stage share LDS");
-
-// Stages this wave's elements at or above xw in LDS (the first SEG of them), in element
-// slot order then lane order; returns how many there are (wave-uniform).
-template <bool BF16, int VEC>
-__device__ __forceinline__ uint32_t stage_cands(const float (&x)[VEC][Elem<BF16>::EPV], float xw, Cand* seg,
-                                                uint32_t c0) {
-    constexpr int EPV = Elem<BF16>::EPV;
-    uint32_t n = 0;
-#pragma unroll
-    for (int q = 0; q < VEC; q++)
-#pragma unroll
-        for (int e = 0; e < EPV; e++) {
-            const bool take = x[q][e] >= xw;
-            const uint64_t bal = __ballot(take);
-            if (bal) {
-                const uint32_t pos =
-                    n + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-                if (take && pos < (uint32_t)SEG) {
-                    seg[pos].idx = c0 + (uint32_t)(q * BLOCK + threadIdx.x) * EPV + e;
-                    seg[pos].x = x[q][e];
-                }
-                n += (uint32_t)__popcll(bal);
-            }
-        }
-    return n;
-}
-
-// The same elements straight to global memory from offset o (a wave with more than SEG).
-template <bool BF16, int VEC>
-__device__ __forceinline__ void emit_cands(const float (&x)[VEC][Elem<BF16>::EPV], float xw, Cand* dst, uint32_t o,
-                                           uint32_t c0) {
-    constexpr int EPV = Elem<BF16>::EPV;
-#pragma unroll
-    for (int q = 0; q < VEC; q++)
-#pragma unroll
-        for (int e = 0; e < EPV; e++) {
-            const bool take = x[q][e] >= xw;
-            const uint64_t bal = __ballot(take);
-            if (bal) {
-                if (take) {
-                    const uint32_t r =
-                        __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-                    dst[o + r].idx = c0 + (uint32_t)(q * BLOCK + threadIdx.x) * EPV + e;
-                    dst[o + r].x = x[q][e];
-                }
-                o += (uint32_t)__popcll(bal);
-            }
-        }
-}
-
-// ---- the kernel --------------------------------------------------------------------------
+static_assert(HBINS <= CHUNK_MAX / 2, "the histogram reuses the count array");
 
 template <bool BF16, int VEC, bool FULL>
 __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int row, int chunk, uint32_t c0,
-                                             uint32_t c1, uint32_t logical, bool tron, uint64_t t0);
+                                             uint32_t c1);
 
 template <bool BF16, int VEC>
 __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
     __shared__ StreamSmem sm;
-
     // workgroups are dispatched round-robin over the 8 XCDs: give each XCD a contiguous
     // range of (row, chunk) so a row's chunks share one L2
     const uint32_t G = gridDim.x, bid = blockIdx.x;
@@ -100,41 +39,29 @@ __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
     const uint32_t logical = xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot;
     const int row = (int)(logical / (uint32_t)a.n_chunks);
     const int chunk = (int)(logical % (uint32_t)a.n_chunks);
-    // phase timestamps (diagnostics) are kept in scalar registers and stored at the end
-    const bool tron = a.trace != nullptr;
-    const uint64_t t0 = tron ? wall_clock64() : 0;
     if (row >= a.n_rows) return;
-
     const uint32_t V = (uint32_t)a.V;
     const uint32_t c0 = (uint32_t)chunk * (uint32_t)a.chunk;
     const uint32_t c1 = min(c0 + (uint32_t)a.chunk, V);
     // a full, aligned chunk (all but a row's last) takes the unconditional path, compiled
     // apart so its vector-by-vector waits are not merged with the guarded loads
     if (a.vec_ok && c1 - c0 == (uint32_t)(BLOCK * VEC * Elem<BF16>::EPV))
-        stream_chunk<BF16, VEC, true>(a, sm, row, chunk, c0, c1, logical, tron, t0);
+        stream_chunk<BF16, VEC, true>(a, sm, row, chunk, c0, c1);
     else
-        stream_chunk<BF16, VEC, false>(a, sm, row, chunk, c0, c1, logical, tron, t0);
+        stream_chunk<BF16, VEC, false>(a, sm, row, chunk, c0, c1);
 }
 
 template <bool BF16, int VEC, bool FULL>
 __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int row, int chunk, uint32_t c0,
-                                             uint32_t c1, uint32_t logical, bool tron, uint64_t t0) {
+                                             uint32_t c1) {
     constexpr int EPV = Elem<BF16>::EPV;
     const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
-    uint64_t ts[8] = {t0, 0, 0, 0, 0, 0, 0, 0};
-#define BFI_STAMP(i)                          \
-    do {                                     \
-        if (tron) ts[(i)] = wall_clock64(); \
-    } while (0)
     const uint32_t em = (1u << EPV) - 1u;
 
     // The loads depend on kernel arguments only and go out first: the row's parameters
     // (scalar loads that queue behind other workgroups' traffic) arrive meanwhile. The
-    // allow-mask words go before the logits, so pass 1 can start on the first vector while
-    // the rest are in flight. A history of at most PREPEN_H ids is applied here
-    // (sample.rs:345-367): its ids go out after the first half of a full chunk's logits, so
-    // that the two scalar loads of the row's offsets they need do not hold up the logits,
-    // and before the second half, so they land while pass 1 is still waiting for data.
+    // allow-mask words go before the logits, so the pass can start on the first vector while
+    // the rest are in flight; the history ids go between the two halves of the logits.
     const HistView hv = row_history(a, row);
     const uint32_t* mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
     uint32_t mwd[VEC];
@@ -161,33 +88,32 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
     }
     if (FULL) load_full_range<BF16, VEC, (VEC + 1) / 2, VEC>(a, row, c0, x);
     else load_tile<BF16, VEC>(a, row, c0, c1, x);
-    BFI_STAMP(1);
     const RowCtx C = make_ctx(a, row);
     if (!C.active) return;  // a verify row past its draft: the loads are dropped
 
     // penalties: the ids inside this chunk are counted in LDS (the barriers pass while the
     // second half of the logits is in flight), then each thread reads the counts of its
-    // elements and pass 1 penalizes them as they arrive
+    // elements and the pass penalizes them as they arrive
     uint32_t cw[VEC][EPV / 2];
     if (C.prepen) {
-        uint4* hc4 = reinterpret_cast<uint4*>(sm.u.hc);
+        uint4* hc4 = reinterpret_cast<uint4*>(sm.hc);
         for (int i = tid; i < CHUNK_MAX / 8; i += BLOCK) hc4[i] = make_uint4(0u, 0u, 0u, 0u);
         __syncthreads();  // cleared before any count lands
 #pragma unroll
         for (int g = 0; g < HPT; g++) {  // 16-bit counts: at most PREPEN_H each
             const uint32_t d = hid[g] - c0;
-            if (hid[g] < c1 && hid[g] >= c0) lds_add(&sm.u.hc[d >> 1], 1u << (16 * (d & 1u)));
+            if (hid[g] < c1 && hid[g] >= c0) lds_add(&sm.hc[d >> 1], 1u << (16 * (d & 1u)));
         }
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < VEC; q++) {
             const uint32_t d0 = (uint32_t)(q * BLOCK + tid) * EPV;
             if constexpr (EPV == 4) {
-                const uint2 v = *reinterpret_cast<const uint2*>(&sm.u.hc[d0 >> 1]);
+                const uint2 v = *reinterpret_cast<const uint2*>(&sm.hc[d0 >> 1]);
                 cw[q][0] = v.x;
                 cw[q][1] = v.y;
             } else {
-                const uint4 v = *reinterpret_cast<const uint4*>(&sm.u.hc[d0 >> 1]);
+                const uint4 v = *reinterpret_cast<const uint4*>(&sm.hc[d0 >> 1]);
                 cw[q][0] = v.x;
                 cw[q][1] = v.y;
                 cw[q][2] = v.z;
@@ -198,16 +124,13 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
 
     ChunkPart part;
     part.pad = 0;
-    part.pad2 = 0;
-    part.raw_m = -__builtin_inff();
     part.raw_arg = 0xFFFFFFFFu;
     part.arg = 0;
-    // pass 1, vector by vector as the loads land: the mask (sample.rs:331-337) and the
-    // penalties in place, the running max (with its first index: greedy rows over the
-    // penalized values, sample.rs:429-439; rows with min_p > 1 over the masked, un-penalized
-    // ones for the min-p fallback, sample.rs:415-422) and the running sum of
-    // exp((x - max) / T) rescaled when the max grows (sample.rs:376-386 sums exp(s - max)).
-    // max(x / T) = max(x) / T for T > 0, so the chunk's exact maximum takes one division.
+    // the pass, vector by vector as the loads land: the mask and the penalties in place,
+    // the running max (with its first index: greedy rows over the penalized values; rows
+    // with min_p > 1 over the masked, un-penalized ones) and the running sum of
+    // exp((x - max) / T) rescaled when the max grows (an estimate of the row's normalizer
+    // that the row kernel uses only to size its candidate gathering).
     const bool track_raw = !C.greedy && (C.min_p > 1.0f);
     const bool track_arg = C.greedy || track_raw;
     const bool sums = !C.greedy;
@@ -254,7 +177,6 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
         }
         m = mn;
     }
-    BFI_STAMP(2);
     // the wave's (max, sum), then the chunk's from the NWAVE wave results (one barrier)
     {
         const float mw = wave_max(m);
@@ -272,11 +194,18 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
             sm.wa[w] = bw.i;
         }
     }
+    // the histogram's bins, cleared while the exchange above settles (the history counts
+    // in the same words are all read by now)
+    const bool want_hist = !C.greedy && (C.kmode || C.pmode) && a.vhist != nullptr;
+    if (want_hist) {
+        if (C.prepen) __syncthreads();
+        for (int i = tid; i < HBINS; i += BLOCK) sm.hc[i] = 0u;
+    }
     __syncthreads();
     float lm = sm.wm[0];
 #pragma unroll
     for (int i = 1; i < NWAVE; i++) lm = fmaxf(lm, sm.wm[i]);
-    part.raw_m = lm;  // the reference point of the sums: the chunk's largest (penalized) logit
+    part.raw_m = lm;  // the chunk's largest (penalized) masked logit: the sums' reference point
     if (track_arg) {
         best = ArgMax{sm.wbv[0], sm.wa[0]};
 #pragma unroll
@@ -284,13 +213,11 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
         part.raw_arg = best.i;
         if (!C.greedy) part.raw_m = best.v;  // min_p > 1: the masked, un-penalized maximum
     }
-    BFI_STAMP(3);
     if (C.greedy) {
         part.m = best.v;
         part.arg = best.i;
         part.sum = 0.0;
-        part.ncand = 0;
-        part.theta = -__builtin_inff();
+        part.xm = best.v;
     } else {
         double ls = 0.0;
         if (lm > -__builtin_inff()) {
@@ -298,107 +225,31 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
             for (int i = 0; i < NWAVE; i++) ls += sm.ws[i] * (double)stream_term(C, sm.wm[i], lm);
         }
         part.sum = ls;
-        const float mc = div_T(lm, C);  // exact (sample.rs:373-375)
-        part.m = mc;
-        const bool kb = C.kmode && C.k <= CAND_CAP;
-        const float margin = 1e-4f + 1e-5f * fabsf(mc);
-        if (!(mc > -__builtin_inff())) {
-            part.ncand = 0;
-            part.theta = -__builtin_inff();
-        } else if (!(C.mmode || kb)) {
-            part.ncand = NCAND_UNBOUNDED;
-            part.theta = __builtin_inff();
-        } else {
-            // min-p bound of this chunk: p >= min_p * max p needs s >= max_s + ln(min_p)
-            float th = __builtin_inff();
-            if (C.mmode) {
-                const float lmp = logf(C.min_p);
-                th = mc + lmp - (margin + 1e-5f * fabsf(lmp));
-            }
-            // candidates are finite elements at or above x_bound(th)
-            float xw = fmaxf(x_bound(C, th), -__FLT_MAX__);
-            Cand* seg = sm.u.stage[w];
-            uint32_t wc = C.mmode ? stage_cands<BF16, VEC>(x, xw, seg, c0) : 0u;
-            BFI_STAMP(4);
-            if (lane == 0) sm.wc[w] = wc;
-            __syncthreads();
-            BFI_STAMP(5);
-            uint32_t cnt = 0, pre = 0;
+        part.m = div_T(lm, C);  // exact (sample.rs:373-375): max(x / T) = max(x) / T
+        part.xm = lm;
+    }
+    if (want_hist) {
+        // bin j: the element lies j/8 .. (j+1)/8 log2-units below the chunk maximum (the
+        // last bin takes everything further down); masked elements are not counted
+        if (lm > -__builtin_inff()) {
+            const float sc = C.rTl * (float)HBIN_PER_LOG2;
 #pragma unroll
-            for (int i = 0; i < NWAVE; i++) {
-                const uint32_t c = sm.wc[i];
-                pre += i < w ? c : 0u;
-                cnt += c;
-            }
-            if (kb && (!C.mmode || cnt > (uint32_t)CAND_CAP)) {
-                // top-k bound: the smallest power-of-two distance below the chunk max
-                // holding k elements, then bisection toward a tight count
-                float d = 0.25f, lo = 0.0f;
-                uint32_t c = 0;
-                int it = 0;
-                for (; it < 18; it++) {
-                    c = block_sum_u(tile_count_ge<BF16, VEC>(x, x_bound(C, mc - d)), sm.ru);
-                    if (c >= (uint32_t)C.k) break;
-                    lo = d;
-                    d *= 2.0f;
-                }
-                float tk;
-                if (c < (uint32_t)C.k) {
-                    tk = -__builtin_inff();
-                } else {
-                    float hi = d;
-                    const uint32_t want = max(2u * (uint32_t)C.k, 64u);
-                    for (int j = 0; j < 12 && c > want; j++) {
-                        const float mid = 0.5f * (lo + hi);
-                        const uint32_t cm = block_sum_u(tile_count_ge<BF16, VEC>(x, x_bound(C, mc - mid)), sm.ru);
-                        if (cm >= (uint32_t)C.k) {
-                            hi = mid;
-                            c = cm;
-                        } else {
-                            lo = mid;
-                        }
+            for (int q = 0; q < VEC; q++)
+#pragma unroll
+                for (int e = 0; e < EPV; e++) {
+                    const float xv = x[q][e];
+                    if (xv > -__builtin_inff()) {
+                        const float f = (lm - xv) * sc;
+                        const uint32_t j = f < (float)(HBINS - 1) ? (uint32_t)f : (uint32_t)(HBINS - 1);
+                        lds_add(&sm.hc[j], 1u);
                     }
-                    tk = mc - hi - margin;
                 }
-                th = C.mmode ? fmaxf(th, tk) : tk;
-                xw = fmaxf(x_bound(C, th), -__FLT_MAX__);
-                wc = stage_cands<BF16, VEC>(x, xw, seg, c0);
-                if (lane == 0) sm.wc2[w] = wc;
-                __syncthreads();
-                cnt = 0;
-                pre = 0;
-#pragma unroll
-                for (int i = 0; i < NWAVE; i++) {
-                    const uint32_t ci = sm.wc2[i];
-                    pre += i < w ? ci : 0u;
-                    cnt += ci;
-                }
-            }
-            part.theta = th;
-            if (cnt > (uint32_t)CAND_CAP) {
-                part.ncand = NCAND_OVERFLOW;
-            } else {
-                // every element whose exact value is >= th (a few just below may come along):
-                // each wave's staged run, copied out at the wave's offset
-                part.ncand = cnt;
-                Cand* dst = a.cands + ((int64_t)row * a.n_chunks + chunk) * CAND_CAP + pre;
-                if (wc <= (uint32_t)SEG) {
-                    for (uint32_t j = (uint32_t)lane; j < wc; j += WAVE) dst[j] = seg[j];
-                } else {
-                    emit_cands<BF16, VEC>(x, xw, dst, 0u, c0);
-                }
-            }
         }
+        __syncthreads();
+        uint32_t* dst = a.vhist + ((int64_t)row * a.n_chunks + chunk) * HBINS;
+        for (int i = tid; i < HBINS; i += BLOCK) dst[i] = sm.hc[i];
     }
-    BFI_STAMP(6);
     if (tid == 0) a.parts[(int64_t)row * a.n_chunks + chunk] = part;
-    BFI_STAMP(7);
-    if (tron && tid == 0) {
-        const int64_t tb = (int64_t)logical * 8;
-#pragma unroll
-        for (int i = 0; i < 8; i++) a.trace[tb + i] = ts[i];
-    }
-#undef BFI_STAMP
 }
 
 // ---- launch ----------------------------------------------------------------------------

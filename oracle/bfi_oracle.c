@@ -338,7 +338,7 @@ int orc_judge(int32_t kind, uint32_t token, const uint32_t *ids, const float *w,
         if (ORC_MUTATE == 11 || ids[j] != d) {
             rid[m] = ids[j];
             rw[m] = w[j];
-            if (w[j] > 0.0f) all_nonpos = 0;
+            if (!(w[j] <= 0.0f)) all_nonpos = 0; /* :90 all(w <= 0): a NaN weight is not <= 0 */
             m++;
         }
     }
