@@ -1,4 +1,4 @@
-// smp_row.hip — the row pass of the gfx950 token sampler: one workgroup of 1024 threads
+// smp_row.hip — the row pass of the gfx950 token sampler: one workgroup of 512 threads
 // per row finishes `target()` and `draw()` (sample.rs:326-427, 312-323) or `judge()`
 // (spec.rs:79-97) with the reference's own f32 results.
 //
@@ -22,7 +22,7 @@
 // twice more for the draw (sum, then the position).
 #include <hip/hip_ext.h>
 
-#define BFI_BLOCK 1024
+#define BFI_BLOCK 512
 #include "smp_common.h"
 #include "smp_exact.h"
 
@@ -30,8 +30,8 @@ namespace bfi {
 
 constexpr int LCAP = 8192;   // candidates held in LDS (beyond: the row's global spill area)
 constexpr int NB = 1024;     // value buckets of a walk
-constexpr int RNV_F32 = 2;   // 16-byte vectors per thread per step of a row stream (f32)
-constexpr int RNV_BF16 = 1;  // (bf16)
+constexpr int RNV_F32 = 4;   // 16-byte vectors per thread per step of a row stream (f32)
+constexpr int RNV_BF16 = 2;  // (bf16)
 
 struct __align__(16) RowSmem {
     uint64_t list[LCAP];   // gathered candidates (id << 32 | bits(x)), then keys, then scratch
@@ -64,7 +64,7 @@ struct HistTabs {
     bool dense;  // counts are in cnt (else, more than GDCAP distinct ids: scanned)
 };
 
-__device__ __noinline__ HistTabs build_hist_tabs(const KArgs& a, RowSmem& sm, const RowCtx& C) {
+__device__ __forceinline__ HistTabs build_hist_tabs(const KArgs& a, RowSmem& sm, const RowCtx& C) {
     HistTabs T{nullptr, nullptr, nullptr, false};
     if (!C.pen_on) return T;
     const int tid = threadIdx.x;
@@ -145,13 +145,6 @@ __device__ __forceinline__ float elem_x(const KArgs& a, const HistTabs& T, const
     return pen_logit(T, C, id, l, allowed, inh);
 }
 
-// exp(s - M) of a penalized masked logit x, as the reference computes it (sample.rs:383):
-// s = x / T rounded (sample.rs:374), then expf of the rounded difference.
-__device__ __forceinline__ float exact_e(const RowCtx& C, float x, float M) {
-    if (!(x > -__builtin_inff())) return 0.0f;
-    const float s = div_T(x, C);
-    return expf_ref(s - M);
-}
 // fl(e / S), correctly rounded (a double quotient of two floats rounds to the float
 // quotient: 53 >= 2 * 24 + 2).
 __device__ __forceinline__ float exact_p(float e, float S) { return (float)((double)e / (double)S); }
@@ -219,73 +212,188 @@ namespace bfi {
 // a threshold th (stop at the first i whose running sum reaches th: sample.rs:318), an
 // excluded index (spec.rs:89: the residual without the draft), and gathering of elements
 // whose d * log2(e) (d = s - M, estimated) is at least gth into the candidate list.
+//
+// A stream is one out-of-line function (its arguments by value, in its own registers), so
+// the kernel's code holds one copy of the loop whatever the number of streams a row needs.
 
-struct StreamCfg {
-    int kind;      // 0: e, 1: p
-    float M;       // the row maximum of s = x / T
-    float S;       // kind 1: the normalizer
-    float th;      // threshold (+inf: none)
-    int64_t excl;  // excluded index (-1: none)
-    bool gather;
-    float gth;     // gather bound on d * log2(e)
+__shared__ RowSmem g_sm;  // the row kernel's LDS
+
+struct StreamArgs {
+    const void* logits;     // the row's first logit
+    const uint32_t* mrow;   // allow-mask row, or null
+    const uint32_t* hbm;    // history bitmap, or null (no penalties)
+    const uint32_t* hpre;   // its popcount prefix and dense counts (frequency extension)
+    const uint32_t* hcnt;
+    const uint32_t* hbase;  // the history itself (counts beyond the dense table)
+    const uint32_t* hext;
+    int64_t hnb, hnx;
+    uint64_t* spill;        // the row's spill area
+    uint64_t* trace;        // the row's 16 diagnostic words, or null
+    uint32_t V;
+    int32_t vec_ok, hdense, fast_div;
+    float T, rT, rTl;
+    float rp, pp, fp;
+    int32_t rep_on, pres_on, freq_on;
+    float M, S, th;
+    int64_t excl;           // excluded index (-1: none)
+    int32_t kind;           // 0: e, 1: p
+    int32_t gather;
+    float gth;              // gather bound on d * log2(e)
 };
 struct StreamOut {
     float cum;     // the sum at the stop (or over the whole row)
     int64_t stop;  // the index where the running sum first reached th, or -1
 };
 
-// Per-state constants of the estimate t ~ 2^(x * log2(e)/T + K): K folds -M * log2(e), the
-// state's unit exponent and (kind 1) -log2(S). The estimate's exponent a differs from
-// log2 of the exact t by at most 2^-24 (6|a| + 6|Kc| + |K| + 5|ue| + 1.5) (the roundings of
-// 1/T, log2(e), the constants and the FMA, against the reference's roundings of x / T,
-// s - M and expf), so its relative error is below rho = 2^-24 (4.5|a| + 4.5|Kc| + |K| +
-// 3.6|ue| + 1.5) + 2^-18, the last term for the hardware exp2; kind 1 adds the division's
-// rounding and log2(S)'s error.
+// Global-memory views of the stream's pointers (they arrive in a by-value struct, where the
+// compiler no longer sees that they point to global memory: generic loads would also count
+// against the LDS counter, so every LDS wait would wait for the logits in flight).
+template <typename T>
+__device__ __forceinline__ const BFI_GLB T* gl(const T* p) {
+    return (const BFI_GLB T*)p;
+}
+template <typename T>
+__device__ __forceinline__ BFI_GLB T* gl(T* p) {
+    return (BFI_GLB T*)p;
+}
+
+// The exact value of a finite masked, penalized logit x: e = expf(fl(fl(x / T) - M))
+// (sample.rs:374, 383), or p = fl(e / S) (sample.rs:388). Out of line: rare, and its code
+// (an f64 division, glibc's expf) should exist once.
+__device__ __noinline__ float exact_value(float x, float T, float rT, int32_t fast_div, float M, float S,
+                                          int32_t kind) {
+    float s;
+    if (fast_div) {
+        const uint32_t ax = __float_as_uint(x) & 0x7FFFFFFFu;
+        const bool ok = !((ax - 1u < 0x0D7FFFFFu) || (ax - 0x71800000u < 0x0E000000u));
+        if (ok) {
+            const float q = x * rT;
+            const float er = __builtin_fmaf(-q, T, x);
+            s = er != er ? q : __builtin_fmaf(er, rT, q);
+        } else {
+            s = x / T;
+        }
+    } else {
+        s = x / T;
+    }
+    const float e = expf_ref(s - M);
+    return kind ? exact_p(e, S) : e;
+}
+
+__device__ __forceinline__ uint32_t sa_count(const StreamArgs& A, uint32_t id) {
+    if (!A.freq_on) return 1u;
+    if (A.hdense) return gl(A.hcnt)[dense_rank(gl(A.hpre)[id >> 5], gl(A.hbm)[id >> 5], id & 31)];
+    uint32_t c = 0;
+    for (int64_t j = 0; j < A.hnb; j++) c += gl(A.hbase)[j] == id;
+    for (int64_t j = 0; j < A.hnx; j++) c += gl(A.hext)[j] == id;
+    return c;
+}
+__device__ __forceinline__ float sa_penalize(const StreamArgs& A, float x, uint32_t id) {
+    Pen P;
+    P.rp = A.rp;
+    P.pp = A.pp;
+    P.fp = A.fp;
+    P.rep_on = A.rep_on;
+    P.pres_on = A.pres_on;
+    P.freq_on = A.freq_on;
+    return penalize(x, sa_count(A, id), P);
+}
+
+// The estimate of t = v / u for an element: the exact s = fl(x / T) (Markstein's corrected
+// quotient, exact for |x| in [2^-100, 2^100) and T in [2^-20, 2^20]) and the exact
+// d = fl(s - M) the reference computes, then exp(d) = 2^(h + l) with h = fl(d log2(e)) and
+// l its rounding error plus log2(e)'s own (both exact by FMA), as exp2(h) (1 + l ln 2).
+// Its relative error against glibc's expf(d) is the hardware exp2's (about an ulp) plus
+// expf's half ulp and the correction's rounding; RHO (2^-19, 16 ulps) bounds it with a wide
+// margin (kind 1 adds fl(1/S) and the product's roundings, and the reference's division's).
+// Elements whose estimate lies within RHO of a rounding boundary, and the few the estimate
+// does not cover (|x| outside the quotient's range, exp2 below the normal range while the
+// running sum is still subnormal), take the exact value.
+constexpr float RHO0 = 0x1p-19f;
+constexpr float RHO1 = 0x1p-19f + 0x1p-21f;
+constexpr float L2E_HI = 1.44269502162933349609375f;      // fl(log2(e))
+constexpr float L2E_LO = 1.925963033500011079e-8f;        // log2(e) - L2E_HI
+constexpr float LN2_F = 0.693147180559945309f;
+
 struct StreamState {
     uint32_t m;
     int32_t ue;
-    float K, R0, gth;
     uint32_t tu;  // threshold in units (0xFFFFFFFF: none)
 };
-__device__ __forceinline__ StreamState stream_state(float s, const StreamCfg& cfg, float Kc, float lS, float th) {
+__device__ __forceinline__ StreamState stream_state(float s, const StreamArgs& A) {
     const SumState ss = sum_state(s);
     StreamState st;
     st.m = ss.m;
     st.ue = ss.ue;
-    st.K = Kc - (float)ss.ue - (cfg.kind ? lS : 0.0f);
-    float r = (4.5f * fabsf(Kc) + fabsf(st.K) + 3.6f * fabsf((float)ss.ue) + 1.5f) * 0x1p-24f + 0x1p-18f;
-    if (cfg.kind) r += (6.0f * fabsf(lS) + 2.0f) * 0x1p-24f;
-    st.R0 = r;
-    st.gth = cfg.gth - (float)ss.ue;
-    st.tu = th < __builtin_inff() ? thresh_units(fmaxf(th, 0.0f), ss.ue) : 0xFFFFFFFFu;
+    st.tu = A.th < __builtin_inff() ? thresh_units(fmaxf(A.th, 0.0f), ss.ue) : 0xFFFFFFFFu;
     return st;
 }
 
-// The exact value of element x (penalized masked logit).
-__device__ __forceinline__ float stream_exact(const RowCtx& C, const StreamCfg& cfg, float x) {
-    const float e = exact_e(C, x, cfg.M);
-    return cfg.kind ? exact_p(e, cfg.S) : e;
-}
-
-// Unit count of element x at the state, exact; tie: the element's rounding depends on the
-// running sum's parity (an event).
-__device__ __forceinline__ uint32_t stream_units(const RowCtx& C, const StreamCfg& cfg, const StreamState& st, float x,
-                                                 float& a_out, bool& tie) {
-    tie = false;
+// Unit estimate of element x at the state: returns RN(t) when certain (amb false), else
+// amb = true (the caller takes the exact value). h receives d log2(e) (the gather test).
+__device__ __forceinline__ uint32_t stream_est(const StreamArgs& A, const StreamState& st, float rS, float x,
+                                               float& h_out, bool& amb) {
     if (!(x > -__builtin_inff())) {  // masked: exp(-inf) = 0 exactly
-        a_out = -__builtin_inff();
+        h_out = -__builtin_inff();
+        amb = false;
         return 0u;
     }
-    const float a = __builtin_fmaf(x, C.rTl, st.K);
-    a_out = a;
-    const float ta = __builtin_amdgcn_exp2f(a);
-    const float q = __builtin_rintf(ta);
-    const float f = fabsf(ta - q);
-    const float rho = __builtin_fmaf(fabsf(a), 4.5f * 0x1p-24f, st.R0);
-    if (__builtin_fmaf(ta, rho, f) < 0.5f && ta < 8388608.0f) return (uint32_t)q;
-    const float t = units_of(stream_exact(C, cfg, x), st.ue);
+    const uint32_t ax = __float_as_uint(x) & 0x7FFFFFFFu;
+    const bool ok = A.fast_div && !((ax - 1u < 0x0D7FFFFFu) || (ax - 0x71800000u < 0x0E000000u));
+    const float q0 = x * A.rT;
+    const float r0 = __builtin_fmaf(-q0, A.T, x);
+    const float sx = __builtin_fmaf(r0, A.rT, q0);
+    const float d = sx - A.M;
+    const float h = d * L2E_HI;
+    const float l = __builtin_fmaf(d, L2E_LO, __builtin_fmaf(d, L2E_HI, -h));
+    h_out = h;
+    const float e0 = __builtin_amdgcn_exp2f(h);
+    float ev = __builtin_fmaf(e0, l * LN2_F, e0);
+    if (A.kind) ev *= rS;
+    const float t = __builtin_ldexpf(ev, -st.ue);
+    const float qf = __builtin_rintf(t);
+    const float f = fabsf(t - qf);
+    amb = !ok || (h < -125.0f && st.ue < -125) || !(__builtin_fmaf(t, A.kind ? RHO1 : RHO0, f) < 0.5f) ||
+          !(t < 8388608.0f);
+    return amb ? 0u : (uint32_t)qf;
+}
+
+// The exact unit count of element x at the state (tie: its rounding depends on the running
+// sum's parity, an event).
+__device__ __forceinline__ uint32_t stream_exact_units(const StreamArgs& A, const StreamState& st, float x,
+                                                       bool& tie) {
+    const float t = units_of(exact_value(x, A.T, A.rT, A.fast_div, A.M, A.S, A.kind), st.ue);
     tie = quant_tie(t);
     return quant_units(t);
+}
+
+// Unit counts of one vector's EPV elements: estimates, then the uncertain ones exactly (a
+// short loop, rarely entered).
+template <int EPV>
+__device__ __forceinline__ void vector_units(const StreamArgs& A, const StreamState& st, float rS,
+                                             const float (&x)[EPV], uint32_t (&u)[EPV], uint32_t& tiem,
+                                             float (&h)[EPV], uint32_t& nex) {
+    uint32_t am = 0;
+#pragma unroll
+    for (int e = 0; e < EPV; e++) {
+        bool amb;
+        u[e] = stream_est(A, st, rS, x[e], h[e], amb);
+        am |= amb ? (1u << e) : 0u;
+    }
+    tiem = 0;
+    while (am) {
+        const int i = __builtin_ctz(am);
+        am &= am - 1u;
+        float xe = x[0];
+#pragma unroll
+        for (int e = 1; e < EPV; e++) xe = e == i ? x[e] : xe;
+        bool tie;
+        const uint32_t ue = stream_exact_units(A, st, xe, tie);
+        nex++;
+#pragma unroll
+        for (int e = 0; e < EPV; e++) u[e] = e == i ? ue : u[e];
+        tiem |= tie ? (1u << i) : 0u;
+    }
 }
 
 template <bool BF16, int NV>
@@ -295,20 +403,75 @@ struct RawT {
     uint32_t pw[NV];
 };
 
-template <bool BF16, int NV>
-__device__ __forceinline__ void row_load(const KArgs& a, const RowCtx& C, const HistTabs& T, uint32_t base,
-                                         RawT<BF16, NV>& r) {
+// The stream's arguments made wave-uniform (scalar registers, uniform branches).
+__device__ __forceinline__ uint64_t rfl64(uint64_t v) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+}
+template <typename T>
+__device__ __forceinline__ T* rflp(T* p) {
+    return (T*)rfl64((uint64_t)p);
+}
+__device__ __forceinline__ int32_t rfli(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float rflf(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
+__device__ __forceinline__ StreamArgs uniform_args(const StreamArgs& A) {
+    StreamArgs U;
+    U.logits = rflp(A.logits);
+    U.mrow = rflp(A.mrow);
+    U.hbm = rflp(A.hbm);
+    U.hpre = rflp(A.hpre);
+    U.hcnt = rflp(A.hcnt);
+    U.hbase = rflp(A.hbase);
+    U.hext = rflp(A.hext);
+    U.hnb = (int64_t)rfl64((uint64_t)A.hnb);
+    U.hnx = (int64_t)rfl64((uint64_t)A.hnx);
+    U.spill = rflp(A.spill);
+    U.trace = rflp(A.trace);
+    U.V = (uint32_t)rfli((int32_t)A.V);
+    U.vec_ok = rfli(A.vec_ok);
+    U.hdense = rfli(A.hdense);
+    U.fast_div = rfli(A.fast_div);
+    U.T = rflf(A.T);
+    U.rT = rflf(A.rT);
+    U.rTl = rflf(A.rTl);
+    U.rp = rflf(A.rp);
+    U.pp = rflf(A.pp);
+    U.fp = rflf(A.fp);
+    U.rep_on = rfli(A.rep_on);
+    U.pres_on = rfli(A.pres_on);
+    U.freq_on = rfli(A.freq_on);
+    U.M = rflf(A.M);
+    U.S = rflf(A.S);
+    U.th = rflf(A.th);
+    U.excl = (int64_t)rfl64((uint64_t)A.excl);
+    U.kind = rfli(A.kind);
+    U.gather = rfli(A.gather);
+    U.gth = rflf(A.gth);
+    return U;
+}
+
+// One step's raw words: the logits (16 bytes per vector), and the allow-mask and history
+// bitmap words of every vector. FULL steps lie inside the row: every load is unconditional
+// (absent tables read the row's own first words, discarded later), so no load is merged
+// with another path and nothing waits for them before they are used. The row's tail step
+// loads element by element.
+template <bool BF16, int NV, bool FULL>
+__device__ __forceinline__ void row_load(const StreamArgs& A, uint32_t base, RawT<BF16, NV>& r) {
     constexpr int EPV = Elem<BF16>::EPV;
     typedef typename Elem<BF16>::T ET;
-    const ET* rp = (const ET*)a.logits + (int64_t)C.row * a.row_stride;
-    const uint32_t V = (uint32_t)a.V;
-    const uint32_t ninf = BF16 ? 0xFF80FF80u : 0xFF800000u;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const BFI_GLB ET* rp = gl((const ET*)A.logits);
+    const uint32_t V = A.V;
+    const BFI_GLB uint32_t* mp = gl(A.mrow ? A.mrow : (const uint32_t*)A.logits);
+    const BFI_GLB uint32_t* pp = gl(A.hbm ? A.hbm : (const uint32_t*)A.logits);
 #pragma unroll
     for (int q = 0; q < NV; q++) {
         const uint32_t id0 = base + (uint32_t)(q * BLOCK + threadIdx.x) * EPV;
-        if (a.vec_ok && id0 + EPV <= V) {
-            r.w[q] = *(const uint4*)(rp + id0);
+        if (FULL) {
+            const u32x4 v = *(const BFI_GLB u32x4*)(rp + id0);
+            r.w[q] = make_uint4(v.x, v.y, v.z, v.w);
         } else {
+            const uint32_t ninf = BF16 ? 0xFF80FF80u : 0xFF800000u;
             uint32_t ww[4] = {ninf, ninf, ninf, ninf};
 #pragma unroll
             for (int e = 0; e < EPV; e++) {
@@ -322,184 +485,238 @@ __device__ __forceinline__ void row_load(const KArgs& a, const RowCtx& C, const 
             }
             r.w[q] = make_uint4(ww[0], ww[1], ww[2], ww[3]);
         }
-        const uint32_t wi = id0 < V ? id0 >> 5 : 0u;
-        r.mw[q] = C.mrow ? C.mrow[wi] : 0xFFFFFFFFu;
-        r.pw[q] = C.pen_on ? T.bm[wi] : 0u;
+        const uint32_t wi = FULL ? id0 >> 5 : (id0 < V ? id0 >> 5 : 0u);
+        r.mw[q] = mp[wi];
+        r.pw[q] = pp[wi];
     }
 }
 
 // Masked, penalized logits of one vector.
 template <bool BF16, int NV>
-__device__ __forceinline__ void row_decode(const RowCtx& C, const HistTabs& T, const RawT<BF16, NV>& r, int q,
-                                           uint32_t id0, float (&x)[Elem<BF16>::EPV]) {
+__device__ __forceinline__ void row_decode(const StreamArgs& A, const RawT<BF16, NV>& r, int q, uint32_t id0,
+                                           float (&x)[Elem<BF16>::EPV]) {
     constexpr int EPV = Elem<BF16>::EPV;
     unpack16<BF16, NV>(r.w[q], x);
     const uint32_t em = (1u << EPV) - 1u;
-    const uint32_t mb = (r.mw[q] >> (id0 & 31)) & em;
-    const uint32_t pb = (r.pw[q] >> (id0 & 31)) & em;
+    const uint32_t mb = A.mrow ? (r.mw[q] >> (id0 & 31)) & em : em;
+    const uint32_t pb = A.hbm ? (r.pw[q] >> (id0 & 31)) & em : 0u;
 #pragma unroll
     for (int e = 0; e < EPV; e++) x[e] = ((mb >> e) & 1u) ? x[e] : -__builtin_inff();
     if (pb) {
 #pragma unroll
         for (int e = 0; e < EPV; e++)
-            if ((pb >> e) & 1u) x[e] = penalize(x[e], hist_count(T, C, id0 + e), C.pen);
+            if ((pb >> e) & 1u) x[e] = sa_penalize(A, x[e], id0 + e);
     }
 }
 
 // Appends (id, x) to the row's candidate list: LDS first, then the row's spill area.
-__device__ __forceinline__ void list_append(const KArgs& a, RowSmem& sm, const RowCtx& C, bool take, uint32_t id,
-                                            float x) {
+__device__ __forceinline__ void list_append(const StreamArgs& A, bool take, uint32_t id, float x) {
     const uint64_t bal = __ballot(take);
     if (!bal) return;
     const int leader = __ffsll((unsigned long long)bal) - 1;
     uint32_t base = 0;
-    if (lane_id() == leader) base = lds_add(&sm.misc[MS_N], (uint32_t)__popcll(bal));
+    if (lane_id() == leader) base = lds_add(&g_sm.misc[MS_N], (uint32_t)__popcll(bal));
     base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
     if (take) {
         const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
         const uint64_t ent = ((uint64_t)id << 32) | __float_as_uint(x);
-        if (pos < (uint32_t)LCAP) sm.list[pos] = ent;
-        else if (pos < (uint32_t)a.V) a.spill[(int64_t)C.row * 4 * a.V + pos] = ent;
+        if (pos < (uint32_t)LCAP) g_sm.list[pos] = ent;
+        else if (pos < A.V) gl(A.spill)[pos] = ent;
     }
 }
 
+// The running state of a stream (every thread holds the same).
+struct StreamRun {
+    StreamState st;
+    uint32_t nex, nslow, nevt;
+    uint64_t tslow, tfast, tmark;
+};
+
+// One step of a stream over the words in r (ids base ..): returns true when it stopped
+// (out filled).
+template <bool BF16, int NV>
+__device__ __forceinline__ bool stream_step(const StreamArgs& A, float rS, const RawT<BF16, NV>& ra, uint32_t base,
+                                            StreamRun& R, StreamOut& out) {
+    RowSmem& sm = g_sm;
+    constexpr int EPV = Elem<BF16>::EPV;
+    const int tid = threadIdx.x;
+    uint32_t qs = 0, tf = 0;
+#pragma unroll
+    for (int q = 0; q < NV; q++) {
+        const uint32_t id0 = base + (uint32_t)(q * BLOCK + tid) * EPV;
+        float xq[EPV];
+        row_decode<BF16, NV>(A, ra, q, id0, xq);
+        uint32_t uq[EPV], tiem;
+        float hq[EPV];
+        vector_units<EPV>(A, R.st, rS, xq, uq, tiem, hq, R.nex);
+#pragma unroll
+        for (int e = 0; e < EPV; e++) {
+            const uint32_t id = id0 + e;
+            const bool ex = (int64_t)id == A.excl;
+            qs = sat_add(qs, ex ? 0u : uq[e]);
+            tf |= (!ex && ((tiem >> e) & 1u)) ? 1u : 0u;
+            if (A.gather) list_append(A, hq[e] >= A.gth && xq[e] > -__builtin_inff(), id, xq[e]);
+        }
+    }
+    uint32_t anytie;
+    const uint32_t tot = block_sum_sat_or(qs, tf, anytie, sm);
+    const uint32_t run = sat_add(R.st.m, tot);
+    if (!anytie && run < M_TOP && run < R.st.tu) {
+        R.st.m = run;
+        if (A.trace) {
+            const uint64_t now = wall_clock64();
+            R.tfast += now - R.tmark;
+            R.tmark = now;
+        }
+        return false;
+    }
+    R.nslow++;
+    // an event in this step: vector by vector, element by element in index order
+#pragma unroll
+    for (int q = 0; q < NV; q++) {
+        const uint32_t id0 = base + (uint32_t)(q * BLOCK + tid) * EPV;
+        float xq[EPV];
+        row_decode<BF16, NV>(A, ra, q, id0, xq);
+        int done = -1;  // positions (thread * EPV + e) of this vector up to here are summed
+#pragma unroll 1
+        for (;;) {
+            uint32_t lp[EPV];
+            bool ev[EPV];
+            uint32_t tt = 0;
+            uint32_t uq[EPV], tiem;
+            float hq[EPV];
+            vector_units<EPV>(A, R.st, rS, xq, uq, tiem, hq, R.nex);
+#pragma unroll
+            for (int e = 0; e < EPV; e++) {
+                const int pos = tid * EPV + e;
+                const bool skip = pos <= done || (int64_t)(id0 + e) == A.excl;
+                ev[e] = !skip && ((tiem >> e) & 1u);
+                tt = sat_add(tt, skip ? 0u : uq[e]);
+                lp[e] = tt;
+            }
+            uint32_t vt;
+            const uint32_t pre = block_excl_scan_sat(tt, vt, sm);
+            uint32_t first = 0xFFFFFFFFu;
+#pragma unroll
+            for (int e = EPV - 1; e >= 0; e--) {
+                const uint32_t r = sat_add(R.st.m, sat_add(pre, lp[e]));
+                if (ev[e] || r >= M_TOP || r >= R.st.tu) first = (uint32_t)(tid * EPV + e);
+            }
+            const uint32_t fw = wave_min_u(first);
+            if (lane_id() == 0) sm.wu2[wave_id()] = fw;
+            __syncthreads();
+            uint32_t f = 0xFFFFFFFFu;
+#pragma unroll
+            for (int w = 0; w < NWAVE; w++) f = min(f, sm.wu2[w]);
+            if (f == 0xFFFFFFFFu) {
+                __syncthreads();
+                R.st.m = sat_add(R.st.m, vt);
+                break;
+            }
+            if ((uint32_t)tid == f / EPV) {
+                const int e = (int)(f % EPV);
+                // the event element's values, selected without indexing registers
+                uint32_t ex = 0u, lpe = 0u;
+                bool eve = false;
+                float xe = 0.0f;
+#pragma unroll
+                for (int k = 0; k < EPV; k++) {
+                    if (k + 1 == e) ex = lp[k];
+                    if (k == e) {
+                        lpe = lp[k];
+                        eve = ev[k];
+                        xe = xq[k];
+                    }
+                }
+                const uint32_t rb4 = R.st.m + pre + ex;  // below 2^24: no event before
+                const uint32_t ra4 = sat_add(R.st.m, sat_add(pre, lpe));
+                float res;
+                uint32_t stop = 0;
+                if (!eve && ra4 < M_TOP) {
+                    res = state_value(ra4, R.st.ue);  // the threshold, inside the binade
+                    stop = 1;
+                } else {
+                    const float sb = state_value(rb4, R.st.ue);
+                    const float v = exact_value(xe, A.T, A.rT, A.fast_div, A.M, A.S, A.kind);
+                    res = sb + v;  // the reference's own rounding of this step
+                    stop = res >= A.th ? 1u : 0u;
+                }
+                sm.mf[MF_S] = res;
+                sm.misc[MS_STOP] = stop;
+            }
+            __syncthreads();
+            const float sn = sm.mf[MF_S];
+            const uint32_t stp = sm.misc[MS_STOP];
+            __syncthreads();
+            if (stp) {
+                out.cum = sn;
+                out.stop = (int64_t)(base + (uint32_t)q * BLOCK * EPV + f);
+                return true;
+            }
+            R.st = stream_state(sn, A);
+            R.nevt++;
+            done = (int)f;
+        }
+    }
+    if (A.trace) {
+        const uint64_t now = wall_clock64();
+        R.tslow += now - R.tmark;
+        R.tmark = now;
+    }
+    return false;
+}
+
 template <bool BF16>
-__device__ __noinline__ StreamOut row_stream(const KArgs& a, RowSmem& sm, const RowCtx& C, const HistTabs& T,
-                                const StreamCfg& cfg) {
+__device__ __noinline__ StreamOut row_stream(const StreamArgs Ain) {
+    const StreamArgs A = uniform_args(Ain);
     constexpr int EPV = Elem<BF16>::EPV;
     constexpr int NV = BF16 ? RNV_BF16 : RNV_F32;
     constexpr uint32_t SPAN = (uint32_t)BLOCK * NV * EPV;
     const int tid = threadIdx.x;
-    const uint32_t V = (uint32_t)a.V;
-    const float Kc = -(cfg.M * 1.44269504088896341f);
-    const float lS = cfg.kind ? __log2f(cfg.S) : 0.0f;
-    StreamState st = stream_state(0.0f, cfg, Kc, lS, cfg.th);
+    const uint32_t V = A.V;
+    const float rS = A.kind ? 1.0f / A.S : 0.0f;
+    StreamRun R;
+    R.st = stream_state(0.0f, A);
+    R.nex = R.nslow = R.nevt = 0;
+    R.tslow = R.tfast = 0;
+    R.tmark = A.trace ? wall_clock64() : 0;
     StreamOut out{0.0f, -1};
-    RawT<BF16, NV> ra, rb;
-    row_load<BF16, NV>(a, C, T, 0u, ra);
-    for (uint32_t base = 0; base < V; base += SPAN) {
-        // the next step's loads go out before this step is worked on
-        if (base + SPAN < V) row_load<BF16, NV>(a, C, T, base + SPAN, rb);
-        uint32_t qs = 0, tf = 0;
-#pragma unroll
-        for (int q = 0; q < NV; q++) {
-            const uint32_t id0 = base + (uint32_t)(q * BLOCK + tid) * EPV;
-            float xq[EPV];
-            row_decode<BF16, NV>(C, T, ra, q, id0, xq);
-#pragma unroll
-            for (int e = 0; e < EPV; e++) {
-                const uint32_t id = id0 + e;
-                float av;
-                bool tie;
-                uint32_t u = stream_units(C, cfg, st, xq[e], av, tie);
-                if ((int64_t)id == cfg.excl) {
-                    u = 0;
-                    tie = false;
-                }
-                qs = sat_add(qs, u);
-                tf |= tie ? 1u : 0u;
-                if (cfg.gather) list_append(a, sm, C, av >= st.gth && xq[e] > -__builtin_inff(), id, xq[e]);
-            }
+    // full steps, each loading the next one's words before it works on its own
+    const uint32_t nfull = A.vec_ok ? V / SPAN : 0u;
+    uint32_t base = 0;
+    if (nfull) {
+        // unrolled by two so no words are copied between buffers; every iteration issues
+        // the same loads (past the last full step they re-read it, from the cache), so the
+        // waits before a step count only the loads issued after its own
+        RawT<BF16, NV> ra, rb;
+        row_load<BF16, NV, true>(A, 0u, ra);
+        for (uint32_t i = 0; i < nfull; i += 2) {
+            const uint32_t b0 = i * SPAN;
+            const uint32_t b1 = min(i + 1, nfull - 1) * SPAN, b2 = min(i + 2, nfull - 1) * SPAN;
+            row_load<BF16, NV, true>(A, b1, rb);
+            if (stream_step<BF16, NV>(A, rS, ra, b0, R, out)) return out;
+            if (i + 1 >= nfull) break;
+            row_load<BF16, NV, true>(A, b2, ra);
+            if (stream_step<BF16, NV>(A, rS, rb, b1, R, out)) return out;
         }
-        uint32_t anytie;
-        const uint32_t tot = block_sum_sat_or(qs, tf, anytie, sm);
-        const uint32_t run = sat_add(st.m, tot);
-        if (!anytie && run < M_TOP && run < st.tu) {
-            st.m = run;
-        } else {
-            // an event in this step: vector by vector, element by element in index order
-#pragma unroll
-            for (int q = 0; q < NV; q++) {
-                const uint32_t id0 = base + (uint32_t)(q * BLOCK + tid) * EPV;
-                float xq[EPV];
-                row_decode<BF16, NV>(C, T, ra, q, id0, xq);
-                int done = -1;  // positions (thread * EPV + e) of this vector up to here are summed
-#pragma unroll 1
-                for (;;) {
-                    uint32_t lp[EPV];
-                    bool ev[EPV];
-                    uint32_t tt = 0;
-#pragma unroll
-                    for (int e = 0; e < EPV; e++) {
-                        const int pos = tid * EPV + e;
-                        float av;
-                        bool tie;
-                        uint32_t u = stream_units(C, cfg, st, xq[e], av, tie);
-                        if (pos <= done || (int64_t)(id0 + e) == cfg.excl) {
-                            u = 0;
-                            tie = false;
-                        }
-                        ev[e] = tie;
-                        tt = sat_add(tt, u);
-                        lp[e] = tt;
-                    }
-                    uint32_t vt;
-                    const uint32_t pre = block_excl_scan_sat(tt, vt, sm);
-                    uint32_t first = 0xFFFFFFFFu;
-#pragma unroll
-                    for (int e = EPV - 1; e >= 0; e--) {
-                        const uint32_t r = sat_add(st.m, sat_add(pre, lp[e]));
-                        if (ev[e] || r >= M_TOP || r >= st.tu) first = (uint32_t)(tid * EPV + e);
-                    }
-                    const uint32_t fw = wave_min_u(first);
-                    if (lane_id() == 0) sm.wu2[wave_id()] = fw;
-                    __syncthreads();
-                    uint32_t f = 0xFFFFFFFFu;
-#pragma unroll
-                    for (int w = 0; w < NWAVE; w++) f = min(f, sm.wu2[w]);
-                    if (f == 0xFFFFFFFFu) {
-                        __syncthreads();
-                        st.m = sat_add(st.m, vt);
-                        break;
-                    }
-                    if ((uint32_t)tid == f / EPV) {
-                        const int e = (int)(f % EPV);
-                        // the event element's values, selected without indexing registers
-                        uint32_t ex = 0u, lpe = 0u;
-                        bool eve = false;
-                        float xe = 0.0f;
-#pragma unroll
-                        for (int k = 0; k < EPV; k++) {
-                            if (k + 1 == e) ex = lp[k];
-                            if (k == e) {
-                                lpe = lp[k];
-                                eve = ev[k];
-                                xe = xq[k];
-                            }
-                        }
-                        const uint32_t rb4 = st.m + pre + ex;  // below 2^24: no event before
-                        const uint32_t ra4 = sat_add(st.m, sat_add(pre, lpe));
-                        float res;
-                        uint32_t stop = 0;
-                        if (!eve && ra4 < M_TOP) {
-                            res = state_value(ra4, st.ue);  // the threshold, inside the binade
-                            stop = 1;
-                        } else {
-                            const float sb = state_value(rb4, st.ue);
-                            const float v = stream_exact(C, cfg, xe);
-                            res = sb + v;  // the reference's own rounding of this step
-                            stop = res >= cfg.th ? 1u : 0u;
-                        }
-                        sm.mf[MF_S] = res;
-                        sm.misc[MS_STOP] = stop;
-                    }
-                    __syncthreads();
-                    const float sn = sm.mf[MF_S];
-                    const uint32_t stp = sm.misc[MS_STOP];
-                    __syncthreads();
-                    if (stp) {
-                        out.cum = sn;
-                        out.stop = (int64_t)(base + (uint32_t)q * BLOCK * EPV + f);
-                        return out;
-                    }
-                    st = stream_state(sn, cfg, Kc, lS, cfg.th);
-                    done = (int)f;
-                }
-            }
-        }
-        if (base + SPAN < V) ra = rb;
+        base = nfull * SPAN;
     }
-    out.cum = state_value(st.m, st.ue);
+    for (; base < V; base += SPAN) {  // the tail (or every step of an unaligned row)
+        RawT<BF16, NV> rt;
+        row_load<BF16, NV, false>(A, base, rt);
+        if (stream_step<BF16, NV>(A, rS, rt, base, R, out)) return out;
+    }
+    out.cum = state_value(R.st.m, R.st.ue);
+    if (A.trace) {
+        const uint32_t tot = block_sum_u(R.nex, g_sm.wu);
+        if (tid == 0) {
+            gl(A.trace)[10] = R.tfast;
+            gl(A.trace)[11] = R.tslow;
+            gl(A.trace)[12] = tot;
+            gl(A.trace)[13] = R.nslow;
+            gl(A.trace)[14] = R.nevt;
+        }
+    }
     return out;
 }
 
@@ -540,7 +757,7 @@ __device__ __forceinline__ uint64_t* list_slot(const KArgs& a, RowSmem& sm, int 
 
 // Turns the gathered (id, x) entries into keys, keeps those with p >= p_lo (> 0), and groups
 // them by bucket. Every thread calls it.
-__device__ __noinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const RowCtx& C, float M, float S, float p_lo,
+__device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const RowCtx& C, float M, float S, float p_lo,
                                bool idxmode) {
     const int tid = threadIdx.x;
     const uint32_t N = min(sm.misc[MS_N], (uint32_t)a.V);
@@ -550,7 +767,8 @@ __device__ __noinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const R
         uint64_t* sl = list_slot(a, sm, C.row, j);
         const uint64_t ent = *sl;
         const uint32_t id = (uint32_t)(ent >> 32);
-        const float p = exact_p(exact_e(C, __uint_as_float((uint32_t)ent), M), S);
+        const float xv = __uint_as_float((uint32_t)ent);
+        const float p = xv > -__builtin_inff() ? exact_value(xv, C.T, C.rT, C.fast_div, M, S, 1) : 0.0f;
         uint64_t key = 0;
         if (p > 0.0f && p >= p_lo) {
             key = make_key(p, id, idxmode);
@@ -609,10 +827,19 @@ __device__ __noinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const R
     }
     __syncthreads();
     {
+        // each thread a run of NB / BLOCK consecutive buckets
+        constexpr int PB = (NB + BLOCK - 1) / BLOCK;
+        uint32_t c = 0;
+#pragma unroll
+        for (int i = 0; i < PB; i++) c += (tid * PB + i < NB) ? sm.bcnt[tid * PB + i] : 0u;
         uint32_t tot;
-        const uint32_t c = tid < NB ? sm.bcnt[tid] : 0u;
-        const uint32_t o = block_excl_scan<uint32_t>(c, sm.wu, tot);
-        if (tid < NB) sm.boff[tid] = o;
+        uint32_t o = block_excl_scan<uint32_t>(c, sm.wu, tot);
+#pragma unroll
+        for (int i = 0; i < PB; i++)
+            if (tid * PB + i < NB) {
+                sm.boff[tid * PB + i] = o;
+                o += sm.bcnt[tid * PB + i];
+            }
     }
     __syncthreads();
     for (uint32_t j = tid; j < N; j += BLOCK) {
@@ -681,10 +908,9 @@ __device__ __forceinline__ void wave_sort_glb(uint64_t* buf, int n) {
 // The n keys of a bucket (at src), sorted descending into a scratch buffer of n2 (a power of
 // two >= n) keys: LDS when they fit, else the row's spill area (its sort scratch).
 // Wave 0; returns the buffer.
-__device__ __forceinline__ uint64_t* sort_bucket(const KArgs& a, RowSmem& sm, int row, const uint64_t* src,
-                                                 uint32_t n, int n2) {
+__device__ __forceinline__ uint64_t* sort_bucket(uint64_t* gscratch, const uint64_t* src, uint32_t n, int n2) {
     const int lane = lane_id();
-    uint64_t* buf = n2 <= LCAP ? sm.list : a.spill + (int64_t)row * 4 * a.V + 2 * (int64_t)a.V;
+    uint64_t* buf = n2 <= LCAP ? g_sm.list : gscratch;
     for (int j = lane; j < n2; j += WAVE) buf[j] = (uint32_t)j < n ? src[j] : 0ull;
     if (n2 <= LCAP) {
         wave_lds_sync();
@@ -774,7 +1000,9 @@ __device__ __forceinline__ bool walk_elems(WalkState& w, uint64_t key, float th,
 }
 
 // The walk, done by wave 0 (the result is broadcast through LDS to every thread).
-__device__ __noinline__ WalkOut walk(const KArgs& a, RowSmem& sm, const ListInfo& L, float th, uint32_t R, uint64_t excl, bool idxmode) {
+__device__ __noinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
+                                     uint64_t* gscratch) {
+    RowSmem& sm = g_sm;
     WalkOut o{0.0f, 0u, 0ull, 0};
     if (wave_id() == 0) {
         const int lane = lane_id();
@@ -823,7 +1051,7 @@ __device__ __noinline__ WalkOut walk(const KArgs& a, RowSmem& sm, const ListInfo
             } else {
                 int n2 = WAVE;
                 while ((uint32_t)n2 < n) n2 <<= 1;
-                const uint64_t* buf = sort_bucket(a, sm, L.row, L.G + o0, n, n2);
+                const uint64_t* buf = sort_bucket(gscratch, L.G + o0, n, n2);
                 for (int j0 = 0; j0 < (int)n && !stopped; j0 += WAVE)
                     stopped = walk_elems(w, buf[j0 + lane], th, R, excl, idxmode, o);
             }
@@ -854,7 +1082,9 @@ __device__ __noinline__ WalkOut walk(const KArgs& a, RowSmem& sm, const ListInfo
 
 // Lists the first `lim` keys in order (ids and probabilities) into the row's target
 // arrays (target_rows' kept list). Wave 0.
-__device__ __noinline__ void list_kept(const KArgs& a, RowSmem& sm, const ListInfo& L, int row, uint32_t lim, bool idxmode) {
+__device__ __noinline__ void list_kept(const ListInfo L, uint32_t* ids, float* probs, uint32_t lim, int32_t idxmode,
+                                      uint64_t* gscratch) {
+    RowSmem& sm = g_sm;
     if (wave_id() == 0) {
         const int lane = lane_id();
         uint32_t w = 0;
@@ -863,13 +1093,13 @@ __device__ __noinline__ void list_kept(const KArgs& a, RowSmem& sm, const ListIn
             if (!n) continue;
             int n2 = WAVE;
             while ((uint32_t)n2 < n) n2 <<= 1;
-            const uint64_t* buf = sort_bucket(a, sm, row, L.G + o0, n, n2);
+            const uint64_t* buf = sort_bucket(gscratch, L.G + o0, n, n2);
             for (uint32_t j = lane; j < n; j += WAVE) {
                 const uint32_t pos = w + j;
                 if (pos < lim) {
                     const uint64_t key = buf[j];
-                    a.t_ids[(int64_t)row * a.t_cap + pos] = key_id(key, idxmode);
-                    a.t_probs[(int64_t)row * a.t_cap + pos] = key_p(key, idxmode);
+                    ids[pos] = key_id(key, idxmode);
+                    probs[pos] = key_p(key, idxmode);
                 }
             }
             w += n;
@@ -887,7 +1117,7 @@ namespace bfi {
 
 // Stores the row's outcome. For spec verify, `verdict` is 1 = Accept, 0 = Reject(token);
 // the last row of a sequence to finish resolves the accepted prefix (spec.rs:140-162).
-__device__ void row_emit(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t token, uint32_t verdict) {
+__device__ __forceinline__ void row_emit(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t token, uint32_t verdict) {
     const int tid = threadIdx.x;
     if (!C.verify) {
         if (tid == 0 && a.out_tok) a.out_tok[C.row] = token;
@@ -923,7 +1153,7 @@ __device__ void row_emit(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t 
 }
 
 // A token target (greedy, min-p fallback): judge is equality (spec.rs:81-82).
-__device__ void finish_token(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t tok) {
+__device__ __forceinline__ void finish_token(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t tok) {
     if (threadIdx.x == 0 && a.t_kind) {
         a.t_kind[C.row] = BFI_SMP_TARGET_TOKEN;
         a.t_kept[C.row] = 0;
@@ -932,7 +1162,7 @@ __device__ void finish_token(const KArgs& a, RowSmem& sm, const RowCtx& C, uint3
     row_emit(a, sm, C, tok, C.judged ? (tok == C.draft ? 1u : 0u) : 1u);
 }
 
-__device__ void target_weights(const KArgs& a, const RowCtx& C, int64_t L, int64_t listed) {
+__device__ __forceinline__ void target_weights(const KArgs& a, const RowCtx& C, int64_t L, int64_t listed) {
     if (threadIdx.x == 0 && a.t_kind) {
         a.t_kind[C.row] = BFI_SMP_TARGET_WEIGHTS;
         a.t_kept[C.row] = (int32_t)min(L, (int64_t)INT32_MAX);
@@ -940,7 +1170,7 @@ __device__ void target_weights(const KArgs& a, const RowCtx& C, int64_t L, int64
     }
 }
 
-__device__ void put_stats(const KArgs& a, const RowCtx& C, float M, float S, float kept, float mode) {
+__device__ __forceinline__ void put_stats(const KArgs& a, const RowCtx& C, float M, float S, float kept, float mode) {
     if (threadIdx.x == 0 && a.t_stats) {
         a.t_stats[C.row * 4 + 0] = M;
         a.t_stats[C.row * 4 + 1] = S;
@@ -952,26 +1182,27 @@ __device__ void put_stats(const KArgs& a, const RowCtx& C, float M, float S, flo
 // ---- row maximum over the penalized values (histories the streaming pass left out) -------
 
 template <bool BF16>
-__device__ __noinline__ ArgMax row_max(const KArgs& a, RowSmem& sm, const RowCtx& C, const HistTabs& T) {
+__device__ __noinline__ ArgMax row_max(const StreamArgs Ain) {
+    const StreamArgs A = uniform_args(Ain);
     constexpr int EPV = Elem<BF16>::EPV;
     constexpr int NV = BF16 ? RNV_BF16 : RNV_F32;
     constexpr uint32_t SPAN = (uint32_t)BLOCK * NV * EPV;
-    const uint32_t V = (uint32_t)a.V;
+    const uint32_t V = A.V;
     ArgMax best{-__builtin_inff(), 0xFFFFFFFFu};
     for (uint32_t base = 0; base < V; base += SPAN) {
         RawT<BF16, NV> r;
-        row_load<BF16, NV>(a, C, T, base, r);
+        row_load<BF16, NV, false>(A, base, r);
 #pragma unroll
         for (int q = 0; q < NV; q++) {
             const uint32_t id0 = base + (uint32_t)(q * BLOCK + threadIdx.x) * EPV;
             float x[EPV];
-            row_decode<BF16, NV>(C, T, r, q, id0, x);
+            row_decode<BF16, NV>(A, r, q, id0, x);
 #pragma unroll
             for (int e = 0; e < EPV; e++)
                 if (id0 + e < V) best = argmax_merge(best, ArgMax{x[e], id0 + e});
         }
     }
-    return block_argmax(best, sm.wf, sm.wu);
+    return block_argmax(best, g_sm.wf, g_sm.wu);
 }
 
 // ---- the gather bound from the streaming pass's histograms ------------------------------
@@ -985,7 +1216,7 @@ __device__ __noinline__ ArgMax row_max(const KArgs& a, RowSmem& sm, const RowCtx
 constexpr int NGRID = 512;
 constexpr double MFIX = 1099511627776.0;  // 2^40: fixed point of the grid masses
 
-__device__ __noinline__ float gather_bound(const KArgs& a, RowSmem& sm, const RowCtx& C, float xmax) {
+__device__ __forceinline__ float gather_bound(const KArgs& a, RowSmem& sm, const RowCtx& C, float xmax) {
     const int tid = threadIdx.x;
     const int nc = a.n_chunks;
     uint32_t* CL = sm.bcnt;
@@ -1041,13 +1272,66 @@ __device__ __noinline__ float gather_bound(const KArgs& a, RowSmem& sm, const Ro
 
 constexpr uint32_t LINF = 0xFFFFFFFFu;
 
+// Phase timestamps of a row (diagnostics): words [n_rows * n_chunks * 8 + row * 16 + i].
+#define BFI_RTRACE(a, C, i)                                                                             \
+    do {                                                                                                \
+        if ((a).trace && threadIdx.x == 0)                                                              \
+            (a).trace[(int64_t)(a).n_rows * (a).n_chunks * 8 + (int64_t)(C).row * 16 + (i)] = wall_clock64(); \
+    } while (0)
+
+// The exact probability of element id (its logit loaded, masked and penalized).
 template <bool BF16>
-__device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
+__device__ __forceinline__ float exact_x_p(const KArgs& a, const HistTabs& T, const RowCtx& C, uint32_t id, float M,
+                                           float S) {
+    const float x = elem_x<BF16>(a, T, C, id);
+    return x > -__builtin_inff() ? exact_value(x, C.T, C.rT, C.fast_div, M, S, 1) : 0.0f;
+}
+
+template <bool BF16>
+__device__ __forceinline__ StreamArgs stream_args(const KArgs& a, const RowCtx& C, const HistTabs& T, float M) {
+    StreamArgs A;
+    A.logits = (const char*)a.logits + (int64_t)C.row * a.row_stride * (BF16 ? 2 : 4);
+    A.mrow = C.mrow;
+    A.hbm = C.pen_on ? T.bm : nullptr;
+    A.hpre = T.pre;
+    A.hcnt = T.cnt;
+    A.hbase = C.h.base;
+    A.hext = C.h.extra;
+    A.hnb = C.h.nbase;
+    A.hnx = C.h.nextra;
+    A.spill = a.spill + (int64_t)C.row * 4 * a.V;
+    A.trace = a.trace ? a.trace + (int64_t)a.n_rows * a.n_chunks * 8 + (int64_t)C.row * 16 : nullptr;
+    A.V = (uint32_t)a.V;
+    A.vec_ok = a.vec_ok;
+    A.hdense = T.dense ? 1 : 0;
+    A.fast_div = C.fast_div ? 1 : 0;
+    A.T = C.T;
+    A.rT = C.rT;
+    A.rTl = C.rTl;
+    A.rp = C.pen.rp;
+    A.pp = C.pen.pp;
+    A.fp = C.pen.fp;
+    A.rep_on = C.pen.rep_on;
+    A.pres_on = C.pen.pres_on;
+    A.freq_on = C.pen.freq_on;
+    A.M = M;
+    A.S = 0.0f;
+    A.th = __builtin_inff();
+    A.excl = -1;
+    A.kind = 0;
+    A.gather = 0;
+    A.gth = 0.0f;
+    return A;
+}
+
+template <bool BF16>
+__device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
     const int tid = threadIdx.x;
     const RowCtx C = make_ctx(a, row);
     if (!C.active) return;  // a verify row past its draft
     const int nc = a.n_chunks;
     const uint32_t V = (uint32_t)a.V;
+    BFI_RTRACE(a, C, 0);
     // 1. chunk results: the row maximum, argmax keys
     float M = -__builtin_inff(), xmax = -__builtin_inff();
     uint64_t gk = 0, rk = 0;
@@ -1069,9 +1353,11 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
     gk = block_max_u64(gk, sm.w64);
     rk = block_max_u64(rk, sm.w64);
     const uint32_t raw_tok = rk ? argmax_of_key(rk).i : 0u;  // min-p fallback (sample.rs:415-422)
+    BFI_RTRACE(a, C, 1);
     const HistTabs T = build_hist_tabs(a, sm, C);
+    BFI_RTRACE(a, C, 2);
     if (C.pen_hash) {  // the streaming pass left the penalties out: the maximum again
-        const ArgMax am = row_max<BF16>(a, sm, C, T);
+        const ArgMax am = row_max<BF16>(stream_args<BF16>(a, C, T, 0.0f));
         xmax = am.v;
         M = C.greedy ? am.v : div_T(am.v, C);
         gk = argmax_key(am.v, am.i);
@@ -1107,23 +1393,31 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
     if (sorted && !C.pen_hash && a.vhist) th = gather_bound(a, sm, C, xmax);
     if (C.mmode) th = fmaxf(th, log2f(C.min_p) - 0x1p-6f);
     const bool list_mode = sorted || C.mmode;
+    BFI_RTRACE(a, C, 3);
     // 3. the normalizer, gathering the candidates on the way
     if (tid == 0) sm.misc[MS_N] = 0u;
     __syncthreads();
-    StreamCfg cfg{0, M, 0.0f, __builtin_inff(), -1, list_mode, th - 0x1p-8f};
-    const float S = row_stream<BF16>(a, sm, C, T, cfg).cum;  // sample.rs:381-386
+    const StreamArgs A0 = stream_args<BF16>(a, C, T, M);
+    uint64_t* const gscr = A0.spill + 2 * (int64_t)a.V;  // the row's global sort scratch
+    StreamArgs cfg = A0;
+    cfg.gather = list_mode ? 1 : 0;
+    cfg.gth = th - (0x1p-8f + (fabsf(M) * 12.0f + 200.0f) * 0x1p-24f);
+    const float S = row_stream<BF16>(cfg).cum;  // sample.rs:381-386
     __syncthreads();
+    BFI_RTRACE(a, C, 4);
+    if (a.trace && tid == 0) a.trace[(int64_t)a.n_rows * nc * 8 + (int64_t)row * 16 + 15] = sm.misc[MS_N];
     bool exhaustive = !(th > -__builtin_inff());
     const float p1 = exact_p(1.0f, S);  // the largest probability (the maximum's e is 1)
     if (sorted) {
         for (int attempt = 0; attempt < 2; attempt++) {
             const float p_lo = exhaustive ? 0.0f : (float)(exp2((double)th) / (double)S * (1.0 + 0x1p-20));
             const ListInfo L = build_list(a, sm, C, M, S, p_lo, false);
+            BFI_RTRACE(a, C, 5);
             // top-p (sample.rs:397-409)
             uint32_t Lp = Lk;
             WalkOut o1{0.0f, 0u, 0ull, 0};
             if (C.pmode) {
-                o1 = walk(a, sm, L, C.top_p, Lk, 0ull, false);
+                o1 = walk(L, C.top_p, Lk, 0ull, 0, gscr);
                 if (o1.how == 1) Lp = o1.rank + 1;
                 else if (o1.how == 0 && !exhaustive) Lp = LINF;
             }
@@ -1139,6 +1433,7 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
                 }
             }
             const uint32_t Lfin = min(Lp, Lm);
+            BFI_RTRACE(a, C, 6);
             if (C.mmode && Lfin == 0) {
                 put_stats(a, C, M, S, 0.0f, 2.0f);
                 finish_token(a, sm, C, raw_tok);
@@ -1148,8 +1443,10 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
                 exhaustive = true;
                 if (tid == 0) sm.misc[MS_N] = 0u;
                 __syncthreads();
-                StreamCfg all{0, M, 0.0f, __builtin_inff(), -1, true, -__builtin_inff()};
-                (void)row_stream<BF16>(a, sm, C, T, all);
+                StreamArgs all = A0;
+                all.gather = 1;
+                all.gth = -__builtin_inff();
+                (void)row_stream<BF16>(all);
                 __syncthreads();
                 continue;
             }
@@ -1161,19 +1458,21 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
                 sum = o1.cum;
                 klast = o1.key;
             } else {
-                const WalkOut o2 = walk(a, sm, L, __builtin_inff(), Lfin, 0ull, false);
+                const WalkOut o2 = walk(L, __builtin_inff(), Lfin, 0ull, 0, gscr);
                 sum = o2.cum;
                 klast = o2.how == 2 ? o2.key : 0ull;
             }
             put_stats(a, C, M, S, sum, 1.0f);
+            BFI_RTRACE(a, C, 7);
             if (!C.judged) {  // draw (sample.rs:312-323)
                 const float r = C.u * fmaxf(sum, 0.0f);
-                const WalkOut o3 = walk(a, sm, L, r, Lfin, 0ull, false);
+                const WalkOut o3 = walk(L, r, Lfin, 0ull, 0, gscr);
                 const uint32_t tok = o3.how ? key_id(o3.key, false) : 0u;
+                BFI_RTRACE(a, C, 8);
                 if (a.t_kind) {
                     const uint32_t lim = (uint32_t)min((int64_t)npos, a.t_cap);
                     target_weights(a, C, Lfin, lim);
-                    if (lim) list_kept(a, sm, L, row, lim, false);
+                    if (lim) list_kept(L, a.t_ids + (int64_t)row * a.t_cap, a.t_probs + (int64_t)row * a.t_cap, lim, 0, gscr);
                 }
                 row_emit(a, sm, C, tok, 1u);
                 return;
@@ -1181,7 +1480,7 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
             // judge (spec.rs:83-95)
             const uint32_t d = C.draft;
             float pd = 0.0f;
-            if (d < V) pd = exact_p(exact_e(C, elem_x<BF16>(a, T, C, d), M), S);
+            if (d < V) pd = exact_x_p<BF16>(a, T, C, d, M, S);
             const uint64_t kd = make_key(pd, d, false);
             const bool dk = pd > 0.0f && (klast == 0ull || kd >= klast);
             const float pdk = dk ? pd : 0.0f;
@@ -1195,9 +1494,9 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
             }
             const uint64_t ex = dk ? kd : 0ull;
             const uint32_t Lr = Lfin - (dk ? 1u : 0u);
-            const WalkOut o4 = walk(a, sm, L, __builtin_inff(), Lr, ex, false);
+            const WalkOut o4 = walk(L, __builtin_inff(), Lr, ex, 0, gscr);
             const float r2 = C.u2 * fmaxf(o4.cum, 0.0f);
-            const WalkOut o5 = walk(a, sm, L, r2, Lr, ex, false);
+            const WalkOut o5 = walk(L, r2, Lr, ex, 0, gscr);
             row_emit(a, sm, C, o5.how ? key_id(o5.key, false) : 0u, 0u);
             return;
         }
@@ -1212,23 +1511,23 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
             finish_token(a, sm, C, raw_tok);
             return;
         }
-        const WalkOut o2 = walk(a, sm, L, __builtin_inff(), L.n, 0ull, true);
+        const WalkOut o2 = walk(L, __builtin_inff(), L.n, 0ull, 1, gscr);
         const float sum = o2.cum;
         put_stats(a, C, M, S, sum, 3.0f);
         if (!C.judged) {
             const float r = C.u * fmaxf(sum, 0.0f);
-            const WalkOut o3 = walk(a, sm, L, r, L.n, 0ull, true);
+            const WalkOut o3 = walk(L, r, L.n, 0ull, 1, gscr);
             if (a.t_kind) {
                 const uint32_t lim = (uint32_t)min((int64_t)L.n, a.t_cap);
                 target_weights(a, C, L.n, lim);
-                if (lim) list_kept(a, sm, L, row, lim, true);
+                if (lim) list_kept(L, a.t_ids + (int64_t)row * a.t_cap, a.t_probs + (int64_t)row * a.t_cap, lim, 1, gscr);
             }
             row_emit(a, sm, C, o3.how ? key_id(o3.key, true) : 0u, 1u);
             return;
         }
         const uint32_t d = C.draft;
         float pd = 0.0f;
-        if (d < V) pd = exact_p(exact_e(C, elem_x<BF16>(a, T, C, d), M), S);
+        if (d < V) pd = exact_x_p<BF16>(a, T, C, d, M, S);
         const bool dk = pd >= thresh && pd > 0.0f;
         const float pdk = dk ? pd : 0.0f;
         if (sum > 0.0f && C.u < exact_p(pdk, sum)) {
@@ -1241,20 +1540,22 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
         }
         const uint64_t ex = dk ? make_key(pd, d, true) : 0ull;
         const uint32_t Lr = L.n - (dk ? 1u : 0u);
-        const WalkOut o4 = walk(a, sm, L, __builtin_inff(), Lr, ex, true);
+        const WalkOut o4 = walk(L, __builtin_inff(), Lr, ex, 1, gscr);
         const float r2 = C.u2 * fmaxf(o4.cum, 0.0f);
-        const WalkOut o5 = walk(a, sm, L, r2, Lr, ex, true);
+        const WalkOut o5 = walk(L, r2, Lr, ex, 1, gscr);
         row_emit(a, sm, C, o5.how ? key_id(o5.key, true) : 0u, 0u);
         return;
     }
     // no filter: the whole row in index order (sample.rs:312-323 over every element)
-    StreamCfg pc{1, M, S, __builtin_inff(), -1, false, 0.0f};
-    const float sum = row_stream<BF16>(a, sm, C, T, pc).cum;
+    StreamArgs pc = A0;
+    pc.kind = 1;
+    pc.S = S;
+    const float sum = row_stream<BF16>(pc).cum;
     put_stats(a, C, M, S, sum, 4.0f);
     if (!C.judged) {
-        StreamCfg dc = pc;
+        StreamArgs dc = pc;
         dc.th = C.u * fmaxf(sum, 0.0f);
-        const StreamOut so = row_stream<BF16>(a, sm, C, T, dc);
+        const StreamOut so = row_stream<BF16>(dc);
         const uint32_t tok = so.stop >= 0 ? (uint32_t)so.stop : V - 1u;
         if (a.t_kind) {
             // the positive entries in index order, up to the cap
@@ -1262,7 +1563,7 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
             for (uint32_t b0 = 0; b0 < V; b0 += BLOCK) {
                 const uint32_t id = b0 + (uint32_t)tid;
                 float p = 0.0f;
-                if (id < V) p = exact_p(exact_e(C, elem_x<BF16>(a, T, C, id), M), S);
+                if (id < V) p = exact_x_p<BF16>(a, T, C, id, M, S);
                 const bool pos = p > 0.0f;
                 uint32_t tot;
                 const uint32_t o = block_excl_scan<uint32_t>(pos ? 1u : 0u, sm.wu, tot);
@@ -1279,28 +1580,27 @@ __device__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
     }
     const uint32_t d = C.draft;
     float pd = 0.0f;
-    if (d < V) pd = exact_p(exact_e(C, elem_x<BF16>(a, T, C, d), M), S);
+    if (d < V) pd = exact_x_p<BF16>(a, T, C, d, M, S);
     if (sum > 0.0f && C.u < exact_p(pd, sum)) {
         row_emit(a, sm, C, d, 1u);
         return;
     }
-    StreamCfg rc = pc;
+    StreamArgs rc = pc;
     rc.excl = d < V ? (int64_t)d : -1;
-    const float sres = row_stream<BF16>(a, sm, C, T, rc).cum;
+    const float sres = row_stream<BF16>(rc).cum;
     if (!(sres > 0.0f)) {  // empty residual, or all of its weights 0
         row_emit(a, sm, C, d, 1u);
         return;
     }
     rc.th = C.u2 * sres;
-    const StreamOut so = row_stream<BF16>(a, sm, C, T, rc);
+    const StreamOut so = row_stream<BF16>(rc);
     const uint32_t last = (d == V - 1u) ? V - 2u : V - 1u;
     row_emit(a, sm, C, so.stop >= 0 ? (uint32_t)so.stop : last, 0u);
 }
 
 template <bool BF16>
 __global__ __launch_bounds__(BLOCK) void k_row(KArgs a) {
-    __shared__ RowSmem sm;
-    row_main<BF16>(a, sm, (int)blockIdx.x);
+    row_main<BF16>(a, g_sm, (int)blockIdx.x);
 }
 
 hipError_t launch_row(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
