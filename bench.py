@@ -3,10 +3,13 @@
 A step is one bfi_smp_sample_rows call (or bfi_smp_verify for C4) over a batch that is
 already resident in HBM. The default workload is C2: B=64 rows of V=151936 f32 logits with
 per-row temperature/top-k/top-p/min-p and repetition/presence/frequency penalties over
-512-id Zipf histories. Output: one JSON line with whole-job rows/s, the HBM roofline of the
-streaming pass (the kernel that moves the bytes; its duration from HIP events recorded in
-its dispatch packets on every 32nd step of the timed region) and the CPU oracle's rows/s on
-this host.
+512-id Zipf histories. The timed steps rotate over copies of the batch that together exceed
+the 256 MiB last-level cache, so every step streams its logits from HBM. A separate
+profiling pass (outside the timed loop) records HIP events in the dispatch packets of each
+kernel of every call: the whole call's time (first kernel's start to last kernel's end)
+gives the headline roofline, each kernel's its own entry. Output: one JSON line with
+whole-job rows/s, the roofline, and the CPU oracle's rows/s on this host (all cores, and
+one core).
 """
 import argparse
 import json
@@ -18,12 +21,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [os.path.join(ROOT, "builderforce-inference_amd"), os.path.join(ROOT, "oracle")]
 
 HBM_PEAK_GBS = 8000.0
-PROFILE_EVERY = 32
 METRIC = "sampled rows/sec + achieved HBM GB/s (% of peak) at B=64, V=151936 fp32"
 WORKLOAD_DESC = {
     "C1": "C1: B=1, V=151936 f32, rep 1.1 over 64 ids, T 0.7 / top-k 40 / top-p 0.95",
     "C2": "C2: B=64, V=151936 f32, per-row T U[0.2,1.5], top-k {0,20,50,100}, top-p U[0.8,1], min-p 0.05, "
           "rep 1.1 + presence 0.5 + frequency 0.3 over 512-id Zipf(1.1) histories",
+    "C2M": "C2M: C2 under packed grammar allow-masks (0.1%-30% allowed, runs 1-64)",
     "C3": "C3: B=32, V=151936 f32, packed allow-mask (0.1%-30% allowed, runs 1-64), T 1.0 / top-p 0.9",
     "C4": "C4: spec verify, 16 seq x (4 drafts + 1) rows, V=151936 f32, T 0.8 / top-p 0.95",
     "C5": "C5: B=256, V=262144 bf16, top-p 0.9 over the full vocabulary, rep 1.05 over 1024-id histories",
@@ -43,15 +46,21 @@ def read_traffic(name):
     return None
 
 
-def cpu_baseline(cfg, seconds):
-    """The oracle (C restatement of the reference sampler) on this host's cores, over whole
-    batches of the same workload until `seconds` have elapsed."""
-    import numpy as np
+def cpu_threads():
+    """The cores this process may run on (its CPU affinity)."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        return max(1, os.cpu_count() or 1)
 
+
+def cpu_baseline(cfg, seconds, threads):
+    """The oracle (C restatement of the reference sampler) on this host, `threads` threads
+    splitting each batch's rows, over whole batches of the same workload until `seconds`
+    have elapsed."""
     import oracle as O
     import workloads
 
-    threads = max(1, min(os.cpu_count() or 1, 16))
     x = cfg["logits"]
     dtype = 1 if cfg["dtype"] == "bf16" else 0
     rows = 0
@@ -81,7 +90,7 @@ def cpu_baseline(cfg, seconds):
     return dict(value=rows / el, unit="rows/s", cores=threads, kind="port",
                 sample=f"{batches} whole batches of the {cfg['name']} workload ({rows} rows, {el:.1f} s) through "
                        f"the C restatement of sample.rs/spec.rs (oracle/bfi_oracle.c), rows split over "
-                       f"{threads} threads")
+                       f"{threads} thread{'s' if threads > 1 else ''}")
 
 
 def bench_mask(args):
@@ -147,8 +156,13 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="C2", choices=sorted(WORKLOAD_DESC))
+    ap.add_argument("--profile-launches", type=int, default=200,
+                    help="calls of the profiling pass (events in every kernel's dispatch), before the timed steps")
+    ap.add_argument("--rotate-mib", type=int, default=320,
+                    help="the timed steps cycle through copies of the logits totalling at least this many MiB "
+                         "(0: one batch, cache-resident)")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a device-to-device copy of 256 MiB (10 launches), the reference "
@@ -187,41 +201,48 @@ def main():
     d = workloads.to_device(cfg, dev)
     smp = bfi_smp.Sampler(0)
     verify = "drafts" in cfg
+    # copies of the logits, together above the last-level cache, one per step in turn
+    batch_bytes = d["logits"].numel() * d["logits"].element_size()
+    ncopy = 1 if args.rotate_mib <= 0 else max(1, -(-(args.rotate_mib << 20) // batch_bytes))
+    logits = [d["logits"]] + [d["logits"].clone() for _ in range(ncopy - 1)]
 
-    def step():
+    def step(i):
+        x = logits[i % ncopy]
         if verify:
-            smp.verify(d["logits"], cfg["rows_per_seq"], d["params"], d["drafts"], d["draft_len"], d["u_pairs"],
+            smp.verify(x, cfg["rows_per_seq"], d["params"], d["drafts"], d["draft_len"], d["u_pairs"],
                        d["u_bonus"], d["out_accepted"], d["out_next"], d["hist"], d["hist_off"], d["mask"])
         else:
-            smp.sample_rows(d["logits"], d["params"], d["u"], d["out"], d["hist"], d["hist_off"], d["mask"])
+            smp.sample_rows(x, d["params"], d["u"], d["out"], d["hist"], d["hist_off"], d["mask"])
 
-    for _ in range(args.warmup):
-        step()
+    for i in range(args.warmup):
+        step(i)
     torch.cuda.synchronize()
-    # Kernel durations come from HIP events recorded in the dispatch packets of every
-    # PROFILE_EVERY-th step of the timed region: events on every step would add about 10 us
-    # of event processing per step to the wall time.
+    # the profiling pass: start/stop events in each kernel's dispatch packet, every launch
+    smp.set_profiling(True)
+    for i in range(args.profile_launches):
+        step(i)
+    smp.set_profiling(False)
+    torch.cuda.synchronize()
+    kern_ms, n = smp.profile()
+    # the timed steps (no events)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        if i % PROFILE_EVERY == 0:
-            smp.set_profiling(True)
-            step()
-            smp.set_profiling(False)
-        else:
-            step()
+        step(i)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    stream_ms, select_ms, n = smp.profile()
 
     rows = cfg["B"]
     ms_step = el * 1e3 / args.steps
     value = rows * args.steps / el
     alg = workloads.algorithmic_bytes(cfg)
-    k_us = stream_ms * 1e3 / max(n, 1)
-    s_us = select_ms * 1e3 / max(n, 1)
-    achieved = alg / (k_us * 1e-6) / 1e9
+    us = {k: v * 1e3 / max(n, 1) for k, v in kern_ms.items()}
     traffic = read_traffic(args.config)
+
+    def gbs(t_us):
+        return round(alg / (t_us * 1e-6) / 1e9, 1) if t_us > 0 else None
+
+    achieved = gbs(us["call"])
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -236,25 +257,28 @@ def main():
         "dtype": "bf16" if cfg["dtype"] == "bf16" else "f32",
         "data": "synthetic (seeded generator, builderforce-inference_amd/workloads.py)",
         "config": {"workload": WORKLOAD_DESC[args.config], "batch_rows": rows, "n_vocab": cfg["V"],
-                   "seed": args.seed},
+                   "seed": args.seed, "rotating_copies": ncopy,
+                   "rotating_mib": round(ncopy * batch_bytes / 2 ** 20, 1)},
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_stream",
-            "achieved": round(achieved, 1),
+            "kernel": "whole call (k_stream + k_quant + k_row, first start to last end)",
+            "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
             "traffic": traffic,
             "algorithmic_bytes": alg,
-            "kernel_us": round(k_us, 3),
+            "call_us": round(us["call"], 3),
             "timed_launches": n,
+            "per_kernel": {k: {"us": round(us[k], 3), "achieved": gbs(us[k]),
+                               "frac": round(gbs(us[k]) / HBM_PEAK_GBS, 4) if us[k] > 0 else None}
+                           for k in ("k_stream", "k_quant", "k_row")},
         },
-        "step_breakdown_us": {"k_stream": round(k_us, 3), "k_select": round(s_us, 3),
-                              "wall": round(ms_step * 1e3, 3)},
         "step_hbm_gbs": round(alg / (ms_step * 1e-3) / 1e9, 1),
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds, cpu_threads())
+        out["cpu_baseline_1core"] = cpu_baseline(cfg, args.cpu_seconds, 1)
     smp.close()
     print(json.dumps(out), flush=True)
 

@@ -59,7 +59,7 @@ def lib():
         L.bfi_smp_trace.argtypes = [P, P, I64]
         L.bfi_smp_trace.restype = I64
         L.bfi_smp_set_profiling.argtypes = [P, I32]
-        L.bfi_smp_profile.argtypes = [P, P, P, P]
+        L.bfi_smp_profile.argtypes = [P, P, P]
         L.bfi_smp_sample_rows.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P]
         L.bfi_smp_target_rows.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P, P, P, P, P, I64, P, P]
         L.bfi_smp_verify.argtypes = [P, P, I32, I64, I64, I64, I64, P, P, P, P, P, P, I64, P, P, P, P, P]
@@ -224,11 +224,12 @@ class Sampler:
         self._check(self._L.bfi_smp_set_profiling(self._ctx, 1 if on else 0), "bfi_smp_set_profiling")
 
     def profile(self):
-        """(stream_ms, select_ms, launches) summed over the launches since the last call."""
-        a, b, n = ctypes.c_double(0), ctypes.c_double(0), ctypes.c_int64(0)
-        self._check(self._L.bfi_smp_profile(self._ctx, ctypes.byref(a), ctypes.byref(b), ctypes.byref(n)),
-                    "bfi_smp_profile")
-        return a.value, b.value, n.value
+        """({k_stream, k_quant, k_row, call}: ms, launches) summed over the launches since the
+        last call ("call": k_stream's start to k_row's end, gaps included)."""
+        ms = (ctypes.c_double * 4)()
+        n = ctypes.c_int64(0)
+        self._check(self._L.bfi_smp_profile(self._ctx, ms, ctypes.byref(n)), "bfi_smp_profile")
+        return {"k_stream": ms[0], "k_quant": ms[1], "k_row": ms[2], "call": ms[3]}, n.value
 
     def sample_rows(self, logits, params, u, out, hist=None, hist_off=None, mask=None, stream=None):
         """logits: cuda [B, V] float32 or bfloat16; params: cuda uint8 [B*32]; u: cuda f32 [B];

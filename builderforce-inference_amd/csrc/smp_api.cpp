@@ -16,15 +16,16 @@
 
 namespace bfi {
 hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+hipError_t launch_quant(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 hipError_t launch_row(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 }
 
 struct bfi_smp_ctx {
     int device = 0;
     std::string err;
-    char* ws = nullptr;  // parts | vhist | row_res | row_pen | spill
+    char* ws = nullptr;  // parts | vhist | row_res | row_pen | spill | rinfo | qpre | qhead | qitem
     size_t ws_size = 0;
-    uint32_t* ctr = nullptr;  // seq_ctr, kept zero between launches
+    uint32_t* ctr = nullptr;  // arrival counters (per row), then seq_ctr; kept zero between launches
     size_t ctr_words = 0;
     bool ctr_dirty = false;
     // staging for bfi_smp_sample_host
@@ -34,7 +35,7 @@ struct bfi_smp_ctx {
     uint64_t* trace = nullptr;
     size_t trace_words = 0, trace_used = 0;
     bool tracing = false;
-    // profiling: per launch, start/stop events recorded in the dispatches of k_stream and k_row
+    // profiling: per launch, start/stop events recorded in the dispatches of its three kernels
     bool profiling = false;
     std::vector<hipEvent_t> ev_pool;
     size_t ev_used = 0;
@@ -77,6 +78,8 @@ struct DeviceGuard {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+constexpr int EV_PER_LAUNCH = 6;  // start/stop of k_stream, k_quant, k_row
+
 
 // Launch shape: 16-byte vectors per thread -> chunk of BLOCK*VEC*EPV elements. The largest
 // chunk that still gives >= 1024 workgroups (4 per CU on 256 CUs); at most 256 chunks/row.
@@ -101,7 +104,7 @@ bool choose_shape(int64_t n_rows, int64_t V, int bf16, Shape& s) {
 }
 
 struct Layout {
-    size_t parts, vhist, row_res, row_pen, spill, total;
+    size_t parts, vhist, row_res, row_pen, spill, rinfo, qpre, qhead, qitem, rowcnt, total;
 };
 
 Layout layout(int64_t n_rows, int64_t V, const Shape& s, int bm_words) {
@@ -117,6 +120,16 @@ Layout layout(int64_t n_rows, int64_t V, const Shape& s, int bm_words) {
     off = align_up(off + (size_t)n_rows * (2 * (size_t)bm_words + bfi::GDCAP) * sizeof(uint32_t), 256);
     L.spill = off;
     off = align_up(off + (size_t)n_rows * 4 * (size_t)V * sizeof(uint64_t), 256);
+    L.rinfo = off;
+    off = align_up(off + (size_t)n_rows * sizeof(bfi::RowInfo), 256);
+    L.qpre = off;
+    off = align_up(off + (size_t)n_rows * s.n_chunks * sizeof(bfi::QPre), 256);
+    L.qhead = off;
+    off = align_up(off + (size_t)n_rows * s.n_chunks * sizeof(bfi::QHead), 256);
+    L.qitem = off;
+    off = align_up(off + (size_t)n_rows * s.n_chunks * (bfi::QWIN + 1) * sizeof(bfi::QItem), 256);
+    L.rowcnt = off;
+    off = align_up(off + (size_t)n_rows * sizeof(uint32_t), 256);
     L.total = off;
     return L;
 }
@@ -217,7 +230,7 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     if (!choose_shape(c.n_rows, c.V, c.dtype == BFI_SMP_BF16, s))
         return fail(ctx, BFI_SMP_EINVAL, "no launch shape for n_vocab %lld", (long long)c.V);
     const Layout L = layout(c.n_rows, c.V, s, bm_words);
-    const size_t ctr_words = verify ? (size_t)c.n_seq : 1;
+    const size_t ctr_words = (size_t)c.n_rows + (verify ? (size_t)c.n_seq : 0);
     int rc = ensure_ws(ctx, L.total, ctr_words, stream);
     if (rc) return rc;
 
@@ -257,7 +270,13 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     a.row_res = (uint32_t*)(ctx->ws + L.row_res);
     a.row_pen = (uint32_t*)(ctx->ws + L.row_pen);
     a.spill = (uint64_t*)(ctx->ws + L.spill);
-    a.seq_ctr = ctx->ctr;
+    a.rinfo = (bfi::RowInfo*)(ctx->ws + L.rinfo);
+    a.qpre = (bfi::QPre*)(ctx->ws + L.qpre);
+    a.qhead = (bfi::QHead*)(ctx->ws + L.qhead);
+    a.qitem = (bfi::QItem*)(ctx->ws + L.qitem);
+    a.rowcnt = (uint32_t*)(ctx->ws + L.rowcnt);
+    a.arrive = ctx->ctr;
+    a.seq_ctr = ctx->ctr + c.n_rows;
     a.bm_words = bm_words;
     a.trace = nullptr;
     if (ctx->tracing) {
@@ -276,25 +295,28 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
         a.trace = ctx->trace;
     }
 
-    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipEvent_t ev[EV_PER_LAUNCH] = {};
     if (ctx->profiling) {
-        if (ctx->ev_used + 4 > ctx->ev_pool.size()) {
-            if (ctx->ev_pool.size() >= 4 * 65536) return fail(ctx, BFI_SMP_EINVAL, "profiling record full: read it");
-            for (int i = 0; i < 4 * 256; i++) {
+        if (ctx->ev_used + EV_PER_LAUNCH > ctx->ev_pool.size()) {
+            if (ctx->ev_pool.size() >= EV_PER_LAUNCH * 65536)
+                return fail(ctx, BFI_SMP_EINVAL, "profiling record full: read it");
+            for (int i = 0; i < EV_PER_LAUNCH * 256; i++) {
                 hipEvent_t x;
                 hipError_t ee = hipEventCreate(&x);
                 if (ee != hipSuccess) return hip_fail(ctx, ee, "hipEventCreate");
                 ctx->ev_pool.push_back(x);
             }
         }
-        for (int i = 0; i < 4; i++) ev[i] = ctx->ev_pool[ctx->ev_used + i];
-        ctx->ev_used += 4;
+        for (int i = 0; i < EV_PER_LAUNCH; i++) ev[i] = ctx->ev_pool[ctx->ev_used + i];
+        ctx->ev_used += EV_PER_LAUNCH;
     }
     const int bf16 = c.dtype == BFI_SMP_BF16;
     hipError_t e = hipSuccess;
     if ((e = bfi::launch_stream(a, bf16, s.vec, stream, ev[0], ev[1])) != hipSuccess)
         return hip_fail(ctx, e, "k_stream launch");
-    if ((e = bfi::launch_row(a, bf16, stream, ev[2], ev[3])) != hipSuccess)
+    if ((e = bfi::launch_quant(a, bf16, s.vec, stream, ev[2], ev[3])) != hipSuccess)
+        return hip_fail(ctx, e, "k_quant launch");
+    if ((e = bfi::launch_row(a, bf16, stream, ev[4], ev[5])) != hipSuccess)
         return hip_fail(ctx, e, "k_row launch");
     return BFI_SMP_OK;
 }
@@ -356,23 +378,24 @@ int bfi_smp_set_profiling(bfi_smp_ctx* ctx, int enabled) {
     return BFI_SMP_OK;
 }
 
-int bfi_smp_profile(bfi_smp_ctx* ctx, double* stream_ms, double* select_ms, int64_t* launches) {
-    if (!ctx || !stream_ms || !select_ms || !launches) return fail(ctx, BFI_SMP_EINVAL, "NULL argument");
+int bfi_smp_profile(bfi_smp_ctx* ctx, double* kernel_ms, int64_t* launches) {
+    if (!ctx || !kernel_ms || !launches) return fail(ctx, BFI_SMP_EINVAL, "NULL argument");
     DeviceGuard g(ctx->device);
-    double a = 0.0, b = 0.0;
-    const size_t n = ctx->ev_used / 4;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    const size_t n = ctx->ev_used / EV_PER_LAUNCH;
     for (size_t i = 0; i < n; i++) {
-        hipEvent_t* e = &ctx->ev_pool[4 * i];
-        hipError_t r = hipEventSynchronize(e[3]);
+        hipEvent_t* e = &ctx->ev_pool[EV_PER_LAUNCH * i];
+        hipError_t r = hipEventSynchronize(e[5]);
         if (r != hipSuccess) return hip_fail(ctx, r, "hipEventSynchronize");
-        float t1 = 0.0f, t2 = 0.0f;
-        if ((r = hipEventElapsedTime(&t1, e[0], e[1])) != hipSuccess) return hip_fail(ctx, r, "hipEventElapsedTime");
-        if ((r = hipEventElapsedTime(&t2, e[2], e[3])) != hipSuccess) return hip_fail(ctx, r, "hipEventElapsedTime");
-        a += t1;
-        b += t2;
+        const int pairs[4][2] = {{0, 1}, {2, 3}, {4, 5}, {0, 5}};
+        for (int k = 0; k < 4; k++) {
+            float t = 0.0f;
+            if ((r = hipEventElapsedTime(&t, e[pairs[k][0]], e[pairs[k][1]])) != hipSuccess)
+                return hip_fail(ctx, r, "hipEventElapsedTime");
+            acc[k] += t;
+        }
     }
-    *stream_ms = a;
-    *select_ms = b;
+    for (int k = 0; k < 4; k++) kernel_ms[k] = acc[k];
     *launches = (int64_t)n;
     ctx->ev_used = 0;
     return BFI_SMP_OK;

@@ -126,6 +126,8 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
     C.pen.rp = P.repeat_penalty;
     C.pen.pp = P.presence_penalty;
     C.pen.fp = P.frequency_penalty;
+    C.pen.rrp = 1.0f / P.repeat_penalty;  // IEEE, once per row
+    C.pen.rdiv = P.repeat_penalty >= 0x1p-20f && P.repeat_penalty <= 0x1p20f;
     C.pen.rep_on = fabsf(P.repeat_penalty - 1.0f) > F32_EPS && H > 0;  // sample.rs:346
     C.pen.pres_on = P.presence_penalty != 0.0f && H > 0;               // sample.rs:360
     C.pen.freq_on = P.frequency_penalty != 0.0f && H > 0;
@@ -137,6 +139,14 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int row) {
     (void)esz;
     C.lrow = (const char*)a.logits;
     return C;
+}
+
+// Rows whose normalizer the quantizing pass summarizes (smp_quant.hip) and the row kernel
+// chains: sampled rows whose penalties the streaming pass applied, whose temperature the
+// estimates cover and whose maximum M (the streaming pass's) is finite. The others (and
+// all-masked rows) take the row kernel's exact stream.
+__device__ __forceinline__ bool quant_row(const RowCtx& C, float M) {
+    return C.active && !C.greedy && !C.pen_hash && C.stream_ok && __builtin_fabsf(M) < __builtin_inff();
 }
 
 // ---- chunk loader ----------------------------------------------------------------------

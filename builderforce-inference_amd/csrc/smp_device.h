@@ -41,6 +41,46 @@ struct ChunkPart {
     uint32_t pad;
 };
 
+// Per row: what the streaming pass's last workgroup of the row derives from all chunks.
+struct RowInfo {
+    float M;        // row maximum of s = x / T (exact; greedy rows: of x)
+    float xmax;     // row maximum of the masked (penalized) logits
+    float th;       // every kept element has (x / T - M) log2(e) above th, before the passes'
+                    // rounding margins (-inf: any; +inf: the row keeps no list)
+    float S_apx;    // approximate normalizer (sum of exp(s - M), the chunk masses)
+    uint64_t gk;    // greedy rows: argmax key of the penalized values
+    uint64_t rk;    // rows with min_p > 1: argmax key of the masked, un-penalized values
+};
+
+// The normalizer's running sum where a chunk starts, as the row finisher predicts it: the
+// approximate mass of the chunks before it, and a lower bound the f32 sum cannot go below
+// (the largest term before the chunk: a sum of non-negative terms, each step rounded to
+// nearest, never falls below any of its terms).
+struct QPre {
+    float P;
+    float lb;
+};
+
+// The quantizing pass's summary of one chunk for the normalizer's chain (smp_quant.hip).
+// In index order the chunk's elements are runs of "certain" elements, all added while the
+// running f32 sum stays in one binade (their sum taken in units of that binade), separated
+// by "window" elements, whose binade or rounding the pass could not settle: those near a
+// binade boundary of the predicted running sum, and ties. Item k holds window element k
+// with its exact exp(s - M) and the run before it; the last item holds the tail run.
+constexpr int QWIN = 4096;          // window elements per chunk (beyond: the chunk is exact)
+constexpr uint32_t QF_EXACT = 1u;   // the row kernel streams this chunk exactly
+constexpr uint32_t QI_NONE = 0xFFFFFFFFu;  // item id of the tail run (no element)
+struct QItem {
+    uint32_t id;   // the window element (QI_NONE: none)
+    float e;       // its exact exp(s - M)
+    uint32_t q;    // units the run before it adds (unit 2^ue)
+    int32_t ue;    // the run's unit exponent (with q == 0: the largest it was checked at)
+};
+struct QHead {
+    uint32_t nwin;   // window elements (items: nwin + 1)
+    uint32_t flags;  // QF_EXACT
+};
+
 // Everything a launch needs; passed by value.
 struct KArgs {
     const void* logits;
@@ -80,7 +120,13 @@ struct KArgs {
     uint32_t* seq_ctr;
     uint32_t* row_res;   // verify: 2 words per row {verdict, token}
     uint32_t* row_pen;   // per row: history bitmap[bm_words] + popcount prefix[bm_words] + counts[GDCAP]
-    uint64_t* spill;     // per row: 4 * V keys (the list beyond LDS, its grouped copy, sort scratch)
+    uint64_t* spill;     // per row: 4 * V keys (the candidate list, its grouped copy, sort scratch)
+    RowInfo* rinfo;      // per row: the streaming pass's row results
+    QPre* qpre;          // per (row, chunk): the running sum's prediction at the chunk's start
+    QHead* qhead;        // per (row, chunk): the quantizing pass's summary
+    QItem* qitem;        // per (row, chunk): QWIN + 1 items
+    uint32_t* arrive;    // per row: chunks done (the last one finishes the row; kept zero)
+    uint32_t* rowcnt;    // per row: candidates gathered by the quantizing pass
     int32_t bm_words;
     int32_t pad1;
     uint64_t* trace;     // optional phase timestamps (wall clock) per workgroup
@@ -114,6 +160,21 @@ __device__ __forceinline__ uint64_t lds_add64(uint64_t* p, uint64_t v) {
 }
 __device__ __forceinline__ uint32_t glb_add(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_add((BFI_GLB uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Device-coherent plain stores and loads (write-through past the non-coherent L2s, read
+// from the coherence point): data one workgroup publishes for another of the same launch.
+// The writer waits for its stores (s_waitcnt) before it counts itself done.
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+    __hip_atomic_store((BFI_GLB uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store((BFI_GLB uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
+    return __hip_atomic_load((const BFI_GLB uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev64(const uint64_t* p) {
+    return __hip_atomic_load((const BFI_GLB uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t glb_or(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_or((BFI_GLB uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -382,6 +443,22 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* scr) {
     return r;
 }
 
+// The previous lane's value of an inclusive scan (lane 0: identity): the exclusive scan
+// without subtracting the lane's own value (which, for floating point, cancels the smaller
+// prefix away when the own value dominates it).
+template <typename T>
+__device__ __forceinline__ T wave_excl_of_incl(T x, T identity) {
+    if constexpr (sizeof(T) == 4) {
+        const T up = __builtin_bit_cast(T, __shfl_up(__builtin_bit_cast(int, x), 1));
+        return lane_id() == 0 ? identity : up;
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, x);
+        const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)u, 1);
+        const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(u >> 32), 1);
+        return lane_id() == 0 ? identity : __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
+}
+
 // Exclusive block scan; `total` receives the block sum. Fixed combination order, so the
 // result is deterministic for floating-point T.
 template <typename T>
@@ -398,7 +475,7 @@ __device__ __forceinline__ T block_excl_scan(T v, T* scr, T& total) {
     }
     __syncthreads();
     total = tot;
-    return pre + x - v;
+    return pre + wave_excl_of_incl(x, (T)0);
 }
 
 // (value, index) argmax with the reference's tie rule (sample.rs:429-439): the first
@@ -446,11 +523,29 @@ __device__ __forceinline__ ArgMax block_argmax(ArgMax a, float* scrv, uint32_t* 
 
 struct Pen {
     float rp, pp, fp;
+    float rrp;   // 1 / rp (IEEE): the corrected reciprocal quotient's reciprocal
     bool rep_on, pres_on, freq_on;
+    bool rdiv;   // rp in [2^-20, 2^20]: x / rp as the corrected reciprocal quotient
 };
 
+// x / d rounded like IEEE division: q = RN(x * r) with r = RN(1/d), e = x - q*d exact under
+// FMA, RN(q + e*r) (Markstein's correction) is the correctly rounded quotient for |x| in
+// [2^-100, 2^100) (or x = 0) and d in [2^-20, 2^20] (checked bit-exhaustively on a strided
+// sample of every float against IEEE division); other operands take IEEE division.
+__device__ __forceinline__ float div_rn(float x, float d, float r, bool d_ok) {
+    const uint32_t ax = __float_as_uint(x) & 0x7FFFFFFFu;
+    const bool x_ok = ((ax - 0x0D800000u) < 0x64000000u) | (ax == 0u);
+    if (d_ok & x_ok) {
+        const float q = x * r;
+        const float e = __builtin_fmaf(-q, d, x);
+        const float s = __builtin_fmaf(e, r, q);
+        return e != e ? q : s;
+    }
+    return x / d;
+}
+
 __device__ __forceinline__ float penalize(float x, uint32_t count, const Pen& P) {
-    if (P.rep_on) x = (x > 0.0f) ? x / P.rp : x * P.rp;  // sample.rs:350-354
+    if (P.rep_on) x = (x > 0.0f) ? div_rn(x, P.rp, P.rrp, P.rdiv) : x * P.rp;  // sample.rs:350-354
     if (P.pres_on) x = x - P.pp;                          // sample.rs:364
     if (P.freq_on) {                                      // extension: two roundings, no FMA
         float fc = P.fp * (float)count;

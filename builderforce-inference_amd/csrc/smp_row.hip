@@ -23,6 +23,7 @@
 #include <hip/hip_ext.h>
 
 #define BFI_BLOCK 512
+#include "smp_chain.h"
 #include "smp_common.h"
 #include "smp_exact.h"
 
@@ -30,6 +31,7 @@ namespace bfi {
 
 constexpr int LCAP = 8192;   // candidates held in LDS (beyond: the row's global spill area)
 constexpr int NB = 1024;     // value buckets of a walk
+constexpr int SORTCAP = 1024;  // candidate lists up to this size are sorted outright
 constexpr int RNV_F32 = 4;   // 16-byte vectors per thread per step of a row stream (f32)
 constexpr int RNV_BF16 = 2;  // (bf16)
 
@@ -39,6 +41,8 @@ struct __align__(16) RowSmem {
     uint32_t bcnt[NB];     // per bucket: element count
     uint32_t boff[NB];     // per bucket: first position in grp
     uint32_t bfill[NB];    // per bucket: fill counter, then scratch
+    uint32_t coff[NCMAX + 1];  // the chain: first item of each chunk
+    uint32_t cflag[NCMAX];     //   and its flags
     uint32_t wu[NWAVE];
     uint32_t wu2[NWAVE];
     float wf[NWAVE];
@@ -48,7 +52,12 @@ struct __align__(16) RowSmem {
     float mf[16];
 };
 
-enum { MS_N = 0, MS_STOP = 1, MS_STOPLO = 2, MS_FLAG = 3, MS_TOK = 4, MS_VERDICT = 5, MS_KIND = 6, MS_LAST = 7 };
+__shared__ RowSmem g_sm;  // the row kernel's LDS
+
+enum {
+    MS_N = 0, MS_STOP = 1, MS_STOPLO = 2, MS_FLAG = 3, MS_TOK = 4, MS_VERDICT = 5, MS_KIND = 6, MS_LAST = 7,
+    MS_NV = 8, MS_CLO = 9, MS_CHI = 10, MS_CNEXT = 11, MS_NFB = 12
+};
 enum { MF_S = 0, MF_CUM = 1 };
 
 // ---- row-wide history tables (global workspace) ---------------------------------------
@@ -64,28 +73,25 @@ struct HistTabs {
     bool dense;  // counts are in cnt (else, more than GDCAP distinct ids: scanned)
 };
 
-__device__ __forceinline__ HistTabs build_hist_tabs(const KArgs& a, RowSmem& sm, const RowCtx& C) {
-    HistTabs T{nullptr, nullptr, nullptr, false};
-    if (!C.pen_on) return T;
+__device__ __noinline__ HistTabs hist_tabs(uint32_t* bm, int32_t nw, uint32_t V, HistView h, int32_t freq_on) {
+    RowSmem& sm = g_sm;
     const int tid = threadIdx.x;
-    const int nw = a.bm_words;
-    uint32_t* bm = a.row_pen + (int64_t)C.row * (2 * (int64_t)nw + GDCAP);
     uint32_t* pre = bm + nw;
     uint32_t* cnt = pre + nw;
     for (int w = tid; w < nw; w += BLOCK) bm[w] = 0u;
-    if (C.pen.freq_on)
+    if (freq_on)
         for (int w = tid; w < GDCAP; w += BLOCK) cnt[w] = 0u;
     __threadfence();
     __syncthreads();
-    const int64_t H = C.h.size();
+    const int64_t H = h.size();
     for (int64_t j = tid; j < H; j += BLOCK) {
-        const uint32_t id = C.h.at(j);
-        if (id < (uint32_t)a.V) glb_or(&bm[id >> 5], 1u << (id & 31));
+        const uint32_t id = h.at(j);
+        if (id < V) glb_or(&bm[id >> 5], 1u << (id & 31));
     }
     __threadfence();
     __syncthreads();
     bool dense = false;
-    if (C.pen.freq_on) {
+    if (freq_on) {
         const int per = (nw + BLOCK - 1) / BLOCK;
         const int w0 = tid * per;
         uint32_t s = 0;
@@ -101,18 +107,25 @@ __device__ __forceinline__ HistTabs build_hist_tabs(const KArgs& a, RowSmem& sm,
         __syncthreads();
         if (dense) {
             for (int64_t j = tid; j < H; j += BLOCK) {
-                const uint32_t id = C.h.at(j);
-                if (id < (uint32_t)a.V) glb_add(&cnt[dense_rank(pre[id >> 5], bm[id >> 5], id & 31)], 1u);
+                const uint32_t id = h.at(j);
+                if (id < V) glb_add(&cnt[dense_rank(pre[id >> 5], bm[id >> 5], id & 31)], 1u);
             }
         }
         __threadfence();
         __syncthreads();
     }
+    HistTabs T;
     T.bm = bm;
     T.pre = pre;
     T.cnt = cnt;
     T.dense = dense;
     return T;
+}
+__device__ __forceinline__ HistTabs build_hist_tabs(const KArgs& a, RowSmem& sm, const RowCtx& C) {
+    (void)sm;
+    if (!C.pen_on) return HistTabs{nullptr, nullptr, nullptr, false};
+    return hist_tabs(a.row_pen + (int64_t)C.row * (2 * (int64_t)a.bm_words + GDCAP), a.bm_words, (uint32_t)a.V, C.h,
+                     C.pen.freq_on ? 1 : 0);
 }
 
 // Occurrences of history id `id` (the frequency extension's count).
@@ -216,7 +229,6 @@ namespace bfi {
 // A stream is one out-of-line function (its arguments by value, in its own registers), so
 // the kernel's code holds one copy of the loop whatever the number of streams a row needs.
 
-__shared__ RowSmem g_sm;  // the row kernel's LDS
 
 struct StreamArgs {
     const void* logits;     // the row's first logit
@@ -227,9 +239,11 @@ struct StreamArgs {
     const uint32_t* hbase;  // the history itself (counts beyond the dense table)
     const uint32_t* hext;
     int64_t hnb, hnx;
-    uint64_t* spill;        // the row's spill area
+    uint64_t* spill;        // the row's spill area (its candidate list)
     uint64_t* trace;        // the row's 16 diagnostic words, or null
     uint32_t V;
+    uint32_t lo, hi;        // the element range streamed
+    float s0;               // the running sum before element lo
     int32_t vec_ok, hdense, fast_div;
     float T, rT, rTl;
     float rp, pp, fp;
@@ -260,7 +274,7 @@ __device__ __forceinline__ BFI_GLB T* gl(T* p) {
 // The exact value of a finite masked, penalized logit x: e = expf(fl(fl(x / T) - M))
 // (sample.rs:374, 383), or p = fl(e / S) (sample.rs:388). Out of line: rare, and its code
 // (an f64 division, glibc's expf) should exist once.
-__device__ __noinline__ float exact_value(float x, float T, float rT, int32_t fast_div, float M, float S,
+__device__ __forceinline__ float exact_value(float x, float T, float rT, int32_t fast_div, float M, float S,
                                           int32_t kind) {
     float s;
     if (fast_div) {
@@ -428,6 +442,9 @@ __device__ __forceinline__ StreamArgs uniform_args(const StreamArgs& A) {
     U.spill = rflp(A.spill);
     U.trace = rflp(A.trace);
     U.V = (uint32_t)rfli((int32_t)A.V);
+    U.lo = (uint32_t)rfli((int32_t)A.lo);
+    U.hi = (uint32_t)rfli((int32_t)A.hi);
+    U.s0 = rflf(A.s0);
     U.vec_ok = rfli(A.vec_ok);
     U.hdense = rfli(A.hdense);
     U.fast_div = rfli(A.fast_div);
@@ -451,10 +468,10 @@ __device__ __forceinline__ StreamArgs uniform_args(const StreamArgs& A) {
 }
 
 // One step's raw words: the logits (16 bytes per vector), and the allow-mask and history
-// bitmap words of every vector. FULL steps lie inside the row: every load is unconditional
-// (absent tables read the row's own first words, discarded later), so no load is merged
-// with another path and nothing waits for them before they are used. The row's tail step
-// loads element by element.
+// bitmap words of every vector. FULL steps lie inside the range: every load is
+// unconditional (absent tables read the row's own first words, discarded later), so no
+// load is merged with another path and nothing waits for them before they are used. The
+// range's first and last steps load element by element; elements outside it read as -inf.
 template <bool BF16, int NV, bool FULL>
 __device__ __forceinline__ void row_load(const StreamArgs& A, uint32_t base, RawT<BF16, NV>& r) {
     constexpr int EPV = Elem<BF16>::EPV;
@@ -475,7 +492,7 @@ __device__ __forceinline__ void row_load(const StreamArgs& A, uint32_t base, Raw
             uint32_t ww[4] = {ninf, ninf, ninf, ninf};
 #pragma unroll
             for (int e = 0; e < EPV; e++) {
-                if (id0 + e >= V) continue;
+                if (id0 + e >= A.hi || id0 + e < A.lo) continue;
                 if (BF16) {
                     const uint32_t b = (uint32_t)rp[id0 + e];
                     ww[e >> 1] = (e & 1) ? (ww[e >> 1] & 0xFFFFu) | (b << 16) : (ww[e >> 1] & 0xFFFF0000u) | b;
@@ -509,7 +526,7 @@ __device__ __forceinline__ void row_decode(const StreamArgs& A, const RawT<BF16,
     }
 }
 
-// Appends (id, x) to the row's candidate list: LDS first, then the row's spill area.
+// Appends (id, x) to the row's candidate list (the first V entries of its spill area).
 __device__ __forceinline__ void list_append(const StreamArgs& A, bool take, uint32_t id, float x) {
     const uint64_t bal = __ballot(take);
     if (!bal) return;
@@ -519,9 +536,7 @@ __device__ __forceinline__ void list_append(const StreamArgs& A, bool take, uint
     base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
     if (take) {
         const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
-        const uint64_t ent = ((uint64_t)id << 32) | __float_as_uint(x);
-        if (pos < (uint32_t)LCAP) g_sm.list[pos] = ent;
-        else if (pos < A.V) gl(A.spill)[pos] = ent;
+        if (pos < A.V) gl(A.spill)[pos] = ((uint64_t)id << 32) | __float_as_uint(x);
     }
 }
 
@@ -673,50 +688,46 @@ __device__ __noinline__ StreamOut row_stream(const StreamArgs Ain) {
     constexpr int NV = BF16 ? RNV_BF16 : RNV_F32;
     constexpr uint32_t SPAN = (uint32_t)BLOCK * NV * EPV;
     const int tid = threadIdx.x;
-    const uint32_t V = A.V;
+    const uint32_t hi = A.hi;
     const float rS = A.kind ? 1.0f / A.S : 0.0f;
     StreamRun R;
-    R.st = stream_state(0.0f, A);
+    R.st = stream_state(A.s0, A);
     R.nex = R.nslow = R.nevt = 0;
     R.tslow = R.tfast = 0;
     R.tmark = A.trace ? wall_clock64() : 0;
     StreamOut out{0.0f, -1};
+    uint32_t base = A.lo & ~(uint32_t)(EPV - 1);
+    if (base != A.lo && base < hi) {  // a range starting inside a vector: a guarded first step
+        RawT<BF16, NV> rt;
+        row_load<BF16, NV, false>(A, base, rt);
+        if (stream_step<BF16, NV>(A, rS, rt, base, R, out)) return out;
+        base += SPAN;
+    }
     // full steps, each loading the next one's words before it works on its own
-    const uint32_t nfull = A.vec_ok ? V / SPAN : 0u;
-    uint32_t base = 0;
+    const uint32_t nfull = A.vec_ok && base < hi ? (hi - base) / SPAN : 0u;
     if (nfull) {
         // unrolled by two so no words are copied between buffers; every iteration issues
         // the same loads (past the last full step they re-read it, from the cache), so the
         // waits before a step count only the loads issued after its own
         RawT<BF16, NV> ra, rb;
-        row_load<BF16, NV, true>(A, 0u, ra);
+        row_load<BF16, NV, true>(A, base, ra);
         for (uint32_t i = 0; i < nfull; i += 2) {
-            const uint32_t b0 = i * SPAN;
-            const uint32_t b1 = min(i + 1, nfull - 1) * SPAN, b2 = min(i + 2, nfull - 1) * SPAN;
+            const uint32_t b0 = base + i * SPAN;
+            const uint32_t b1 = base + min(i + 1, nfull - 1) * SPAN, b2 = base + min(i + 2, nfull - 1) * SPAN;
             row_load<BF16, NV, true>(A, b1, rb);
             if (stream_step<BF16, NV>(A, rS, ra, b0, R, out)) return out;
             if (i + 1 >= nfull) break;
             row_load<BF16, NV, true>(A, b2, ra);
             if (stream_step<BF16, NV>(A, rS, rb, b1, R, out)) return out;
         }
-        base = nfull * SPAN;
+        base += nfull * SPAN;
     }
-    for (; base < V; base += SPAN) {  // the tail (or every step of an unaligned row)
+    for (; base < hi; base += SPAN) {  // the tail (or every step of an unaligned row)
         RawT<BF16, NV> rt;
         row_load<BF16, NV, false>(A, base, rt);
         if (stream_step<BF16, NV>(A, rS, rt, base, R, out)) return out;
     }
     out.cum = state_value(R.st.m, R.st.ue);
-    if (A.trace) {
-        const uint32_t tot = block_sum_u(R.nex, g_sm.wu);
-        if (tid == 0) {
-            gl(A.trace)[10] = R.tfast;
-            gl(A.trace)[11] = R.tslow;
-            gl(A.trace)[12] = tot;
-            gl(A.trace)[13] = R.nslow;
-            gl(A.trace)[14] = R.nevt;
-        }
-    }
     return out;
 }
 
@@ -733,11 +744,12 @@ namespace bfi {
 // the keys into NB buckets by the key's high bits; within a bucket they stay unsorted.
 
 struct ListInfo {
-    const uint64_t* G;  // keys grouped by bucket (LDS or the row's spill area)
-    uint32_t n;         // keys in G (candidates with p >= p_safe, and for min-p p >= thresh)
+    const uint64_t* G;  // keys grouped by bucket (LDS or the row's spill area); small: sorted
+    uint32_t n;         // keys in G (candidates with p >= p_lo > 0)
     uint32_t nb;        // buckets in use
     uint64_t kmax;      // the largest key
     int row;
+    int small;          // n <= SORTCAP: the keys sorted in LDS (G = the LDS list), no buckets
 };
 
 __device__ __forceinline__ float key_p(uint64_t key, bool idxmode) {
@@ -751,69 +763,121 @@ __device__ __forceinline__ uint64_t make_key(float p, uint32_t id, bool idxmode)
                    : (((uint64_t)(0x80000000u | __float_as_uint(p)) << 32) | (uint64_t)(~id));
 }
 
-__device__ __forceinline__ uint64_t* list_slot(const KArgs& a, RowSmem& sm, int row, uint32_t j) {
-    return j < (uint32_t)LCAP ? &sm.list[j] : &a.spill[(int64_t)row * 4 * a.V + j];
-}
-
-// Turns the gathered (id, x) entries into keys, keeps those with p >= p_lo (> 0), and groups
-// them by bucket. Every thread calls it.
-__device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const RowCtx& C, float M, float S, float p_lo,
-                               bool idxmode) {
+// Turns the N gathered (id, x) entries of the row's list into keys, keeps those with
+// p >= p_lo (> 0), compacted (LDS, then the row's spill area from 2V), and groups them by
+// bucket; at most WAVE keys are sorted by one wave instead. Every thread calls it.
+__device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t N, float M,
+                                               float S, float p_lo, bool idxmode) {
     const int tid = threadIdx.x;
-    const uint32_t N = min(sm.misc[MS_N], (uint32_t)a.V);
-    uint32_t hmax = 0u, hmin = 0xFFFFFFFFu, nv = 0;
+    const uint64_t* src = a.spill + (int64_t)C.row * 4 * a.V;
+    uint64_t* ovf = a.spill + (int64_t)C.row * 4 * a.V + 2 * (int64_t)a.V;
+    N = min(N, (uint32_t)a.V);
+    if (tid == 0) sm.misc[MS_NV] = 0u;
+    __syncthreads();
+    uint32_t hmax = 0u, hmin = 0xFFFFFFFFu;
     uint64_t kmax = 0;
     for (uint32_t j = tid; j < N; j += BLOCK) {
-        uint64_t* sl = list_slot(a, sm, C.row, j);
-        const uint64_t ent = *sl;
+        const uint64_t ent = src[j];
         const uint32_t id = (uint32_t)(ent >> 32);
         const float xv = __uint_as_float((uint32_t)ent);
         const float p = xv > -__builtin_inff() ? exact_value(xv, C.T, C.rT, C.fast_div, M, S, 1) : 0.0f;
-        uint64_t key = 0;
-        if (p > 0.0f && p >= p_lo) {
-            key = make_key(p, id, idxmode);
+        const bool valid = p > 0.0f && p >= p_lo;
+        const uint64_t key = make_key(p, id, idxmode);
+        const uint64_t bal = __ballot(valid);
+        if (!bal) continue;
+        const int leader = __ffsll((unsigned long long)bal) - 1;
+        uint32_t base = 0;
+        if (lane_id() == leader) base = lds_add(&sm.misc[MS_NV], (uint32_t)__popcll(bal));
+        base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
+        if (valid) {
+            const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
+            if (pos < (uint32_t)LCAP) sm.list[pos] = key;
+            else ovf[pos] = key;
             const uint32_t hi = (uint32_t)(key >> 32);
             hmax = max(hmax, hi);
             hmin = min(hmin, hi);
             kmax = key > kmax ? key : kmax;
-            nv++;
         }
-        *sl = key;
     }
+    __threadfence_block();
+    __syncthreads();
+    const uint32_t nv = sm.misc[MS_NV];
     ListInfo L;
-    // reductions: max/min of the high words, the largest key, the count
+    L.n = nv;
+    L.row = C.row;
+    L.nb = 0;
+    if (nv <= (uint32_t)WAVE) {
+        // small: one wave sorts the keys into LDS
+        L.small = 1;
+        L.G = sm.list;
+        if (wave_id() == 0) {
+            const int lane = lane_id();
+            uint64_t key = (uint32_t)lane < nv ? sm.list[lane] : 0ull;
+            key = wave_sort_desc(key);
+            sm.list[lane] = key;
+            if (lane == 0) sm.w64[0] = key;
+        }
+        __syncthreads();
+        L.kmax = sm.w64[0];
+        __syncthreads();
+        return L;
+    }
+    if (nv <= (uint32_t)SORTCAP) {
+        // medium: a block-wide bitonic sort (descending) of the keys, zero-padded to a power
+        // of two, in LDS
+        L.small = 1;
+        L.G = sm.list;
+        uint32_t n2 = WAVE;
+        while (n2 < nv) n2 <<= 1;
+        for (uint32_t j = nv + (uint32_t)tid; j < n2; j += BLOCK) sm.list[j] = 0ull;
+        __syncthreads();
+        for (uint32_t size = 2; size <= n2; size <<= 1) {
+            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                for (uint32_t i = (uint32_t)tid; i < n2 / 2; i += BLOCK) {
+                    const uint32_t lo = 2 * i - (i & (stride - 1));
+                    const uint32_t hi = lo + stride;
+                    const bool desc = (lo & size) == 0;
+                    const uint64_t x = sm.list[lo], y = sm.list[hi];
+                    if ((x < y) == desc) {
+                        sm.list[lo] = y;
+                        sm.list[hi] = x;
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        L.kmax = sm.list[0];
+        __syncthreads();
+        return L;
+    }
+    L.small = 0;
+    // reductions: max/min of the high words, the largest key
     {
         const uint32_t wmx = lane63(wave_scan_incl(hmax, 0u, [](uint32_t x, uint32_t y) { return max(x, y); }));
         const uint32_t wmn = wave_min_u(hmin);
         const uint64_t wk = wave_max_u64(kmax);
-        const uint32_t wn = wave_sum_u(nv);
         if (lane_id() == 0) {
             sm.wu[wave_id()] = wmx;
             sm.wu2[wave_id()] = wmn;
             sm.w64[wave_id()] = wk;
-            sm.wf[wave_id()] = __uint_as_float(wn);
         }
         __syncthreads();
         hmax = 0u;
         hmin = 0xFFFFFFFFu;
         kmax = 0;
-        nv = 0;
 #pragma unroll
         for (int w = 0; w < NWAVE; w++) {
             hmax = max(hmax, sm.wu[w]);
             hmin = min(hmin, sm.wu2[w]);
             kmax = sm.w64[w] > kmax ? sm.w64[w] : kmax;
-            nv += __float_as_uint(sm.wf[w]);
         }
         __syncthreads();
     }
     int sh = idxmode ? 0 : 18;
-    if (nv) while ((hmax >> sh) - (hmin >> sh) >= (uint32_t)NB) sh++;
+    while ((hmax >> sh) - (hmin >> sh) >= (uint32_t)NB) sh++;
     const uint32_t top = hmax >> sh;
-    L.nb = nv ? top - (hmin >> sh) + 1 : 0;
-    L.n = nv;
+    L.nb = top - (hmin >> sh) + 1;
     L.kmax = kmax;
-    L.row = C.row;
     uint64_t* G = nv <= (uint32_t)LCAP ? sm.grp : a.spill + (int64_t)C.row * 4 * a.V + a.V;
     L.G = G;
     for (int b = tid; b < NB; b += BLOCK) {
@@ -821,9 +885,9 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
         sm.bfill[b] = 0u;
     }
     __syncthreads();
-    for (uint32_t j = tid; j < N; j += BLOCK) {
-        const uint64_t key = *list_slot(a, sm, C.row, j);
-        if (key) lds_add(&sm.bcnt[top - ((uint32_t)(key >> 32) >> sh)], 1u);
+    for (uint32_t j = tid; j < nv; j += BLOCK) {
+        const uint64_t key = j < (uint32_t)LCAP ? sm.list[j] : ovf[j];
+        lds_add(&sm.bcnt[top - ((uint32_t)(key >> 32) >> sh)], 1u);
     }
     __syncthreads();
     {
@@ -842,12 +906,10 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
             }
     }
     __syncthreads();
-    for (uint32_t j = tid; j < N; j += BLOCK) {
-        const uint64_t key = *list_slot(a, sm, C.row, j);
-        if (key) {
-            const uint32_t b = top - ((uint32_t)(key >> 32) >> sh);
-            G[sm.boff[b] + lds_add(&sm.bfill[b], 1u)] = key;
-        }
+    for (uint32_t j = tid; j < nv; j += BLOCK) {
+        const uint64_t key = j < (uint32_t)LCAP ? sm.list[j] : ovf[j];
+        const uint32_t b = top - ((uint32_t)(key >> 32) >> sh);
+        G[sm.boff[b] + lds_add(&sm.bfill[b], 1u)] = key;
     }
     __threadfence_block();
     __syncthreads();
@@ -1000,7 +1062,7 @@ __device__ __forceinline__ bool walk_elems(WalkState& w, uint64_t key, float th,
 }
 
 // The walk, done by wave 0 (the result is broadcast through LDS to every thread).
-__device__ __noinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
+__device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
                                      uint64_t* gscratch) {
     RowSmem& sm = g_sm;
     WalkOut o{0.0f, 0u, 0ull, 0};
@@ -1010,8 +1072,10 @@ __device__ __noinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uin
         walk_set(w, 0.0f, th);
         w.r = 0;
         bool stopped = false;
+        for (uint32_t j0 = 0; L.small && j0 < L.n && !stopped; j0 += WAVE)
+            stopped = walk_elems(w, j0 + (uint32_t)lane < L.n ? sm.list[j0 + lane] : 0ull, th, R, excl, idxmode, o);
         uint32_t b0 = 0;
-        while (b0 < L.nb && !stopped) {
+        while (!L.small && b0 < L.nb && !stopped) {
             const uint32_t b = b0 + (uint32_t)lane;
             const uint32_t cnt = b < L.nb ? sm.bcnt[b] : 0u;
             const uint32_t off = b < L.nb ? sm.boff[b] : 0u;
@@ -1082,10 +1146,16 @@ __device__ __noinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uin
 
 // Lists the first `lim` keys in order (ids and probabilities) into the row's target
 // arrays (target_rows' kept list). Wave 0.
-__device__ __noinline__ void list_kept(const ListInfo L, uint32_t* ids, float* probs, uint32_t lim, int32_t idxmode,
+__device__ __forceinline__ void list_kept(const ListInfo L, uint32_t* ids, float* probs, uint32_t lim, int32_t idxmode,
                                       uint64_t* gscratch) {
     RowSmem& sm = g_sm;
-    if (wave_id() == 0) {
+    if (L.small) {
+        for (uint32_t j = (uint32_t)threadIdx.x; j < lim; j += BLOCK) {
+            const uint64_t key = sm.list[j];
+            ids[j] = key_id(key, idxmode);
+            probs[j] = key_p(key, idxmode);
+        }
+    } else if (wave_id() == 0) {
         const int lane = lane_id();
         uint32_t w = 0;
         for (uint32_t b = 0; b < L.nb && w < lim; b++) {
@@ -1205,67 +1275,144 @@ __device__ __noinline__ ArgMax row_max(const StreamArgs Ain) {
     return block_argmax(best, g_sm.wf, g_sm.wu);
 }
 
-// ---- the gather bound from the streaming pass's histograms ------------------------------
+// ---- the normalizer from the quantizing pass's chunk summaries ---------------------------
 //
-// Bin j of chunk c holds the elements j/8 .. (j+1)/8 log2-units below the chunk maximum
-// xm_c, which lies o_c = (xmax - xm_c) log2(e)/T below the row's. On a grid of bounds
-// theta_g = -g/8 (in log2-units of exp(s - M)) this gives lower bounds on the count and on
-// the mass exp(s - M) of the elements above theta_g (bins entirely above it). The bound is
-// the highest theta_g whose lower bound reaches k (top-k) or the top-p mass with margins
-// for the reference's rounding (sample.rs:397-409); every kept element lies above it.
-constexpr int NGRID = 512;
-constexpr double MFIX = 1099511627776.0;  // 2^40: fixed point of the grid masses
+// The chunks' items (smp_quant.hip) in index order: the run before each window element, the
+// element, and each chunk's tail run. Wave 0 walks them 64 at a time from the running sum's
+// exact state (m, ue): a run adds its units in one step when the state lies in the run's
+// binade (a zero run: in its binade or above) and stays below the binade's top; a window
+// element adds RN(e / u) units unless it is a tie or leaves the binade, in which case it is
+// one real f32 addition (the reference's rounding of that step). A run that fails its check
+// (a prediction the f32 sum's drift outran) and a chunk the pass left exact are re-streamed
+// exactly (row_stream) from the state before them to the chunk's end; the walk continues at
+// the next chunk. The items are staged in LDS (the grouped-key array, free at this point).
 
-__device__ __forceinline__ float gather_bound(const KArgs& a, RowSmem& sm, const RowCtx& C, float xmax) {
+constexpr int QSTAGE = (int)(sizeof(RowSmem::grp) / (sizeof(QItem)));  // items the grouped-key array holds
+
+
+// The chunk heads: item offsets and flags into LDS; returns the item count. Every thread.
+__device__ __forceinline__ uint32_t chain_heads(const QHead* heads, int nc, RowSmem& sm) {
     const int tid = threadIdx.x;
-    const int nc = a.n_chunks;
-    uint32_t* CL = sm.bcnt;
-    uint64_t* ML = sm.grp;
-    for (int g = tid; g < NGRID; g += BLOCK) {
-        CL[g] = 0u;
-        ML[g] = 0ull;
+    uint32_t n = 0;
+    if (tid < nc) {
+        const QHead h = heads[tid];
+        sm.cflag[tid] = h.flags;
+        n = (h.flags & QF_EXACT) ? 1u : h.nwin + 1u;
     }
+    uint32_t tot;
+    const uint32_t pre = block_excl_scan<uint32_t>(n, sm.wu, tot);
+    if (tid < nc) sm.coff[tid] = pre;
+    if (tid == 0) sm.coff[nc] = tot;
     __syncthreads();
-    double sapprox = 0.0;
-    const float eps = 0x1p-8f;
-    for (int idx = tid; idx < nc * HBINS; idx += BLOCK) {
-        const int c = idx / HBINS, j = idx % HBINS;
-        const ChunkPart& P = a.parts[(int64_t)C.row * nc + c];
-        const float xm = P.xm;
-        if (!(xm > -__builtin_inff())) continue;
-        const float o = (xmax - xm) * C.rTl;
-        if (j == 0) sapprox += P.sum * exp2((double)-o);
-        const uint32_t cnt = a.vhist[((int64_t)C.row * nc + c) * HBINS + j];
-        if (!cnt || j == HBINS - 1) continue;
-        const float glo = ceilf(8.0f * o + (float)(j + 1) + 8.0f * eps);
-        if (glo < (float)NGRID) {
-            const int g = (int)glo;
-            lds_add(&CL[g], cnt);
-            const double m = (double)cnt * exp2(-(double)o - (double)(j + 1) / 8.0 - (double)eps);
-            lds_add64(&ML[g], (uint64_t)(m * MFIX));
+    return tot;
+}
+
+// Largest chunk c in [lo, hi) with coff[c] <= g.
+__device__ __forceinline__ int chunk_of(const RowSmem& sm, int lo, int hi, uint32_t g) {
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (sm.coff[mid] <= g) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+struct ChainIO {
+    float s;        // the running sum at item `next`
+    uint32_t next;  // the item to continue at
+    uint32_t lo, hi;  // out: elements to re-stream exactly from s (lo == hi: none)
+};
+
+// Walks the items from io.next until all are done (lo == hi) or a range must be re-streamed.
+// Every thread calls it.
+__device__ __forceinline__ ChainIO chain_walk(const QItem* items, int32_t nc, uint32_t chunk, uint32_t V,
+                                           uint32_t total, ChainIO io, uint64_t* tr) {
+    RowSmem& sm = g_sm;
+    const int tid = threadIdx.x;
+    QItem* const stage = reinterpret_cast<QItem*>(sm.grp);
+    items = rflp(items);
+    tr = rflp(tr);
+    nc = rfli(nc);
+    chunk = (uint32_t)rfli((int32_t)chunk);
+    V = (uint32_t)rfli((int32_t)V);
+    total = (uint32_t)rfli((int32_t)total);
+    float s = rflf(io.s);
+    uint32_t next = (uint32_t)rfli((int32_t)io.next);
+    while (next < total) {
+        // stage the chunks from the one holding `next` while their items fit
+        const int sc0 = chunk_of(sm, 0, nc, next);
+        const uint32_t base = sm.coff[sc0];
+        int sc1 = chunk_of(sm, sc0, nc + 1, base + (uint32_t)QSTAGE);
+        if (sc1 <= sc0) sc1 = sc0 + 1;
+        const uint32_t n = sm.coff[sc1] - base;
+        constexpr int PER = QSTAGE / BLOCK;
+        QItem v[PER];
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            const uint32_t g = (uint32_t)(r * BLOCK + tid);
+            if (g < n) {
+                const int c = chunk_of(sm, sc0, sc1, base + g);
+                if (sm.cflag[c] & QF_EXACT) {
+                    v[r] = QItem{QI_EXACT, 0.0f, 0u, (int32_t)(((uint32_t)c << 16))};
+                } else {
+                    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                    const u32x4 it = *(const BFI_GLB u32x4*)(items + (int64_t)c * (QWIN + 1) + (base + g - sm.coff[c]));
+                    v[r] = QItem{it.x, __uint_as_float(it.y), it.z, (int32_t)(((uint32_t)c << 16) | (it.w & 0xFFFFu))};
+                }
+            }
         }
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            const uint32_t g = (uint32_t)(r * BLOCK + tid);
+            if (g < n) stage[g] = v[r];
+        }
+        __syncthreads();
+        if (tr && tid == 0 && !gl(tr)[12]) gl(tr)[12] = wall_clock64();  // diagnostics: staged
+        if (wave_id() == 0) {
+            const int lane = lane_id();
+            const SumState st0 = sum_state(s);
+            uint32_t m = st0.m;
+            int32_t ue = st0.ue;
+            const uint32_t hit = chain_run([&](uint32_t j) { return stage[j]; }, next - base, n, V, m, ue);
+            uint32_t flo = 0, fhi = 0, fnext = 0, fb = 0;
+            if (hit < n) {
+                // re-stream from the start of this item's run (after the previous window of
+                // its chunk, else the chunk's start) to the chunk's end
+                const QItem hi = stage[hit];
+                const uint32_t c = item_chunk((uint32_t)hi.ue);
+                if (tr && lane == 0) {  // diagnostics: why the walk left the summaries
+                    const int sh = hi.id == QI_EXACT ? 0 : (item_ue((uint32_t)hi.ue) != ue ? 16 : 32);
+                    gl(tr)[14] = gl(tr)[14] + (1ull << sh);
+                    gl(tr)[13] = ((uint64_t)c << 48) | ((uint64_t)(hit - sm.coff[c] + base) << 32) |
+                                ((uint64_t)(item_ue((uint32_t)hi.ue) & 0xFFFF) << 16) | (uint64_t)(ue & 0xFFFF);
+                    gl(tr)[12] = ((uint64_t)hi.q << 32) | m;
+                }
+                uint32_t lo = c * chunk;
+                if (hi.id != QI_EXACT && hit > 0) {
+                    const QItem pv = stage[hit - 1];
+                    if (item_chunk((uint32_t)pv.ue) == c && pv.id < V) lo = pv.id + 1u;
+                }
+                flo = lo;
+                fhi = min((c + 1u) * chunk, V);
+                fnext = sm.coff[c + 1];
+                fb = 1;
+            }
+            if (tr && lane == 0 && !gl(tr)[13]) gl(tr)[13] = wall_clock64();  // diagnostics: walked
+            if (lane == 0) {
+                sm.mf[MF_S] = state_value(m, ue);
+                sm.misc[MS_CLO] = flo;
+                sm.misc[MS_CHI] = fhi;
+                sm.misc[MS_CNEXT] = fb ? fnext : base + n;
+            }
+        }
+        __syncthreads();
+        s = sm.mf[MF_S];
+        const uint32_t flo = sm.misc[MS_CLO], fhi = sm.misc[MS_CHI];
+        next = sm.misc[MS_CNEXT];
+        __syncthreads();
+        if (fhi > flo) return ChainIO{s, next, flo, fhi};  // (an empty range needs no stream)
     }
-    const double S_hi = block_sum_d(sapprox, sm.wd) * (1.0 + 1e-4);
-    __syncthreads();
-    // inclusive prefixes over the grid
-    uint32_t cl = tid < NGRID ? CL[tid] : 0u;
-    uint64_t ml = tid < NGRID ? ML[tid] : 0ull;
-    uint32_t ct;
-    uint64_t mt;
-    cl += block_excl_scan<uint32_t>(cl, sm.wu, ct);
-    ml += block_excl_scan<uint64_t>(ml, sm.w64, mt);
-    uint32_t gk = 0xFFFFFFFFu, gp = 0xFFFFFFFFu;
-    if (tid < NGRID) {
-        if (C.kmode && cl >= (uint32_t)C.k) gk = (uint32_t)tid;
-        const double tgt = (double)min(C.top_p * 1.01f + 3e-4f, 2.0f) * S_hi * MFIX;
-        if (C.pmode && (double)ml >= tgt) gp = (uint32_t)tid;
-    }
-    gk = block_min_u(gk, sm.wu);
-    gp = block_min_u(gp, sm.wu);
-    float th = -__builtin_inff();
-    if (C.kmode && gk != 0xFFFFFFFFu) th = fmaxf(th, -(float)gk / 8.0f);
-    if (C.pmode && gp != 0xFFFFFFFFu) th = fmaxf(th, -(float)gp / 8.0f);
-    return th;
+    return ChainIO{s, next, 0u, 0u};
 }
 
 // ---- the row kernel ----------------------------------------------------------------------
@@ -1287,6 +1434,24 @@ __device__ __forceinline__ float exact_x_p(const KArgs& a, const HistTabs& T, co
     return x > -__builtin_inff() ? exact_value(x, C.T, C.rT, C.fast_div, M, S, 1) : 0.0f;
 }
 
+// The same without the history tables: the block counts id's occurrences in the history
+// (sample.rs:345-367 penalize a history id once per occurrence count). Every thread.
+template <bool BF16>
+__device__ __forceinline__ float scan_x_p(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t id, float M,
+                                          float S) {
+    uint32_t c = 0;
+    if (C.pen_on) {
+        const int64_t H = C.h.size();
+        for (int64_t j = threadIdx.x; j < H; j += BLOCK) c += C.h.at(j) == id ? 1u : 0u;
+        c = block_sum_u(c, sm.wu);
+    }
+    const float l = load_logit<BF16>(a, C.row, id);
+    const bool allowed = !C.mrow || ((C.mrow[id >> 5] >> (id & 31)) & 1u);
+    float x = allowed ? l : -__builtin_inff();
+    if (c) x = penalize(x, c, C.pen);
+    return x > -__builtin_inff() ? exact_value(x, C.T, C.rT, C.fast_div, M, S, 1) : 0.0f;
+}
+
 template <bool BF16>
 __device__ __forceinline__ StreamArgs stream_args(const KArgs& a, const RowCtx& C, const HistTabs& T, float M) {
     StreamArgs A;
@@ -1302,6 +1467,9 @@ __device__ __forceinline__ StreamArgs stream_args(const KArgs& a, const RowCtx& 
     A.spill = a.spill + (int64_t)C.row * 4 * a.V;
     A.trace = a.trace ? a.trace + (int64_t)a.n_rows * a.n_chunks * 8 + (int64_t)C.row * 16 : nullptr;
     A.V = (uint32_t)a.V;
+    A.lo = 0u;
+    A.hi = (uint32_t)a.V;
+    A.s0 = 0.0f;
     A.vec_ok = a.vec_ok;
     A.hdense = T.dense ? 1 : 0;
     A.fast_div = C.fast_div ? 1 : 0;
@@ -1332,36 +1500,25 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
     const int nc = a.n_chunks;
     const uint32_t V = (uint32_t)a.V;
     BFI_RTRACE(a, C, 0);
-    // 1. chunk results: the row maximum, argmax keys
-    float M = -__builtin_inff(), xmax = -__builtin_inff();
-    uint64_t gk = 0, rk = 0;
-    for (int c = tid; c < nc; c += BLOCK) {
-        const ChunkPart P = a.parts[(int64_t)row * nc + c];
-        M = fmaxf(M, P.m);
-        xmax = fmaxf(xmax, P.xm);
-        if (C.greedy) {
-            const uint64_t k = argmax_key(P.m, P.arg);
-            gk = k > gk ? k : gk;
-        }
-        if (C.min_p > 1.0f) {
-            const uint64_t k = argmax_key(P.raw_m, P.raw_arg);
-            rk = k > rk ? k : rk;
-        }
-    }
-    M = block_max(M, sm.wf);
-    xmax = block_max(xmax, sm.wf);
-    gk = block_max_u64(gk, sm.w64);
-    rk = block_max_u64(rk, sm.w64);
+    // 1. the row results of the streaming pass: maximum, argmax keys, candidate bound
+    const RowInfo& RI = a.rinfo[row];
+    float M = ld_uniform(&RI.M);
+    const float th = ld_uniform(&RI.th);
+    uint64_t gk = ld_uniform(&RI.gk);
+    const uint64_t rk = ld_uniform(&RI.rk);
     const uint32_t raw_tok = rk ? argmax_of_key(rk).i : 0u;  // min-p fallback (sample.rs:415-422)
+    // the history tables, built when a stream or a lookup needs them
+    HistTabs T{nullptr, nullptr, nullptr, false};
+    bool tabs = false;
     BFI_RTRACE(a, C, 1);
-    const HistTabs T = build_hist_tabs(a, sm, C);
-    BFI_RTRACE(a, C, 2);
     if (C.pen_hash) {  // the streaming pass left the penalties out: the maximum again
+        T = build_hist_tabs(a, sm, C);
+        tabs = true;
         const ArgMax am = row_max<BF16>(stream_args<BF16>(a, C, T, 0.0f));
-        xmax = am.v;
         M = C.greedy ? am.v : div_T(am.v, C);
         gk = argmax_key(am.v, am.i);
     }
+    BFI_RTRACE(a, C, 2);
     if (C.greedy) {  // sample.rs:369-371
         const ArgMax am = argmax_of_key(gk);
         finish_token(a, sm, C, am.v > -__builtin_inff() ? am.i : 0u);
@@ -1387,31 +1544,66 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
         }
         return;
     }
-    // 2. the gather bound (log2-units below the maximum)
     const bool sorted = C.kmode || C.pmode;
-    float th = -__builtin_inff();
-    if (sorted && !C.pen_hash && a.vhist) th = gather_bound(a, sm, C, xmax);
-    if (C.mmode) th = fmaxf(th, log2f(C.min_p) - 0x1p-6f);
     const bool list_mode = sorted || C.mmode;
+    const float gth = th - (0x1p-8f + (fabsf(M) * 12.0f + 200.0f) * 0x1p-24f);
     BFI_RTRACE(a, C, 3);
-    // 3. the normalizer, gathering the candidates on the way
-    if (tid == 0) sm.misc[MS_N] = 0u;
-    __syncthreads();
-    const StreamArgs A0 = stream_args<BF16>(a, C, T, M);
-    uint64_t* const gscr = A0.spill + 2 * (int64_t)a.V;  // the row's global sort scratch
-    StreamArgs cfg = A0;
-    cfg.gather = list_mode ? 1 : 0;
-    cfg.gth = th - (0x1p-8f + (fabsf(M) * 12.0f + 200.0f) * 0x1p-24f);
-    const float S = row_stream<BF16>(cfg).cum;  // sample.rs:381-386
-    __syncthreads();
+    // 2. the normalizer (sample.rs:381-386) and the candidate list
+    float S;
+    uint32_t N = 0;
+    if (quant_row(C, M)) {
+        // the quantizing pass's chunk summaries, chained; it gathered the candidates
+        const uint32_t total = chain_heads(a.qhead + (int64_t)row * nc, nc, sm);
+        BFI_RTRACE(a, C, 10);
+        ChainIO io{0.0f, 0u, 0u, 0u};
+        uint32_t nfb = 0;
+        for (;;) {
+            io = chain_walk(a.qitem + (int64_t)row * nc * (QWIN + 1), nc, (uint32_t)a.chunk, V, total, io,
+                            a.trace ? a.trace + (int64_t)a.n_rows * nc * 8 + (int64_t)row * 16 : nullptr);
+            if (io.hi <= io.lo) {
+                if (io.next >= total) break;
+                continue;
+            }
+            if (!tabs) {
+                T = build_hist_tabs(a, sm, C);
+                tabs = true;
+            }
+            StreamArgs fb = stream_args<BF16>(a, C, T, M);
+            fb.lo = io.lo;
+            fb.hi = io.hi;
+            fb.s0 = io.s;
+            io.s = row_stream<BF16>(fb).cum;
+            nfb++;
+            __syncthreads();
+        }
+        S = io.s;
+        BFI_RTRACE(a, C, 11);
+        if (a.trace && tid == 0) a.trace[(int64_t)a.n_rows * nc * 8 + (int64_t)row * 16 + 9] = nfb;
+        N = list_mode ? ld_uniform(a.rowcnt + row) : 0u;
+    } else {
+        // the whole row streamed exactly, gathering the candidates on the way
+        if (!tabs) {
+            T = build_hist_tabs(a, sm, C);
+            tabs = true;
+        }
+        if (tid == 0) sm.misc[MS_N] = 0u;
+        __syncthreads();
+        StreamArgs cfg = stream_args<BF16>(a, C, T, M);
+        cfg.gather = list_mode ? 1 : 0;
+        cfg.gth = gth;
+        S = row_stream<BF16>(cfg).cum;
+        __syncthreads();
+        N = sm.misc[MS_N];
+    }
     BFI_RTRACE(a, C, 4);
-    if (a.trace && tid == 0) a.trace[(int64_t)a.n_rows * nc * 8 + (int64_t)row * 16 + 15] = sm.misc[MS_N];
+    if (a.trace && tid == 0) a.trace[(int64_t)a.n_rows * nc * 8 + (int64_t)row * 16 + 15] = N;
+    uint64_t* const gscr = a.spill + (int64_t)row * 4 * a.V + 2 * (int64_t)a.V;  // the row's sort scratch
     bool exhaustive = !(th > -__builtin_inff());
     const float p1 = exact_p(1.0f, S);  // the largest probability (the maximum's e is 1)
     if (sorted) {
         for (int attempt = 0; attempt < 2; attempt++) {
             const float p_lo = exhaustive ? 0.0f : (float)(exp2((double)th) / (double)S * (1.0 + 0x1p-20));
-            const ListInfo L = build_list(a, sm, C, M, S, p_lo, false);
+            const ListInfo L = build_list(a, sm, C, N, M, S, p_lo, false);
             BFI_RTRACE(a, C, 5);
             // top-p (sample.rs:397-409)
             uint32_t Lp = Lk;
@@ -1441,13 +1633,18 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
             }
             if (Lfin == LINF || (Lfin > L.n && !exhaustive)) {  // the list does not reach the cut
                 exhaustive = true;
+                if (!tabs) {
+                    T = build_hist_tabs(a, sm, C);
+                    tabs = true;
+                }
                 if (tid == 0) sm.misc[MS_N] = 0u;
                 __syncthreads();
-                StreamArgs all = A0;
+                StreamArgs all = stream_args<BF16>(a, C, T, M);
                 all.gather = 1;
                 all.gth = -__builtin_inff();
                 (void)row_stream<BF16>(all);
                 __syncthreads();
+                N = sm.misc[MS_N];
                 continue;
             }
             const uint32_t npos = min(Lfin, L.n);  // kept elements with p > 0
@@ -1480,7 +1677,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
             // judge (spec.rs:83-95)
             const uint32_t d = C.draft;
             float pd = 0.0f;
-            if (d < V) pd = exact_x_p<BF16>(a, T, C, d, M, S);
+            if (d < V) pd = scan_x_p<BF16>(a, sm, C, d, M, S);
             const uint64_t kd = make_key(pd, d, false);
             const bool dk = pd > 0.0f && (klast == 0ull || kd >= klast);
             const float pdk = dk ? pd : 0.0f;
@@ -1505,7 +1702,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
     const float thresh = C.mmode ? C.min_p * p1 : 0.0f;
     if (C.mmode && thresh > 0.0f) {
         // min-p alone: the kept elements in index order (sample.rs:411-414)
-        const ListInfo L = build_list(a, sm, C, M, S, thresh, true);
+        const ListInfo L = build_list(a, sm, C, N, M, S, thresh, true);
         if (L.n == 0) {
             put_stats(a, C, M, S, 0.0f, 2.0f);
             finish_token(a, sm, C, raw_tok);
@@ -1527,7 +1724,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
         }
         const uint32_t d = C.draft;
         float pd = 0.0f;
-        if (d < V) pd = exact_x_p<BF16>(a, T, C, d, M, S);
+        if (d < V) pd = scan_x_p<BF16>(a, sm, C, d, M, S);
         const bool dk = pd >= thresh && pd > 0.0f;
         const float pdk = dk ? pd : 0.0f;
         if (sum > 0.0f && C.u < exact_p(pdk, sum)) {
@@ -1547,7 +1744,11 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
         return;
     }
     // no filter: the whole row in index order (sample.rs:312-323 over every element)
-    StreamArgs pc = A0;
+    if (!tabs) {
+        T = build_hist_tabs(a, sm, C);
+        tabs = true;
+    }
+    StreamArgs pc = stream_args<BF16>(a, C, T, M);
     pc.kind = 1;
     pc.S = S;
     const float sum = row_stream<BF16>(pc).cum;

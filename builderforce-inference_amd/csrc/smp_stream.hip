@@ -8,7 +8,10 @@
 // x / T (sample.rs:373-379), the first index of the maximum for greedy rows (sample.rs:
 // 429-439) and of the un-penalized maximum for the min-p fallback (sample.rs:415-422), an
 // approximate f64 mass, and for top-k / top-p rows a 128-bucket histogram of how far below
-// the chunk maximum its elements lie. The row kernel (smp_row.hip) takes it from there.
+// the chunk maximum its elements lie. The last workgroup of a row to finish (an arrival
+// counter) combines the chunks: the row maximum, the approximate normalizer mass before
+// each chunk (the quantizing pass's prediction of the running sum, smp_quant.hip) and the
+// bound the kept set lies above (the candidates the passes after it gather).
 #include <hip/hip_ext.h>
 
 #include "smp_common.h"
@@ -20,10 +23,157 @@ struct __align__(16) StreamSmem {
     float wm[NWAVE];    // per-wave maxima of the masked logits
     float wbv[NWAVE];   // per-wave argmax value (greedy rows: penalized; min_p > 1: raw)
     uint32_t wa[NWAVE]; // per-wave first index of that value
+    uint32_t last;      // this workgroup finishes the row
+    uint32_t pad[3];
+    float xm[NCMAX];    // the row finisher: each chunk's maximum
     uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids, two 16-bit halves a word;
-                                 // then the histogram (HBINS words)
+                                 // then the histogram (HBINS words); the row finisher's grids
 };
 static_assert(HBINS <= CHUNK_MAX / 2, "the histogram reuses the count array");
+
+constexpr int NGRID = 512;                // gather-bound grid: bounds -g/8 log2-units, g < NGRID
+constexpr double MFIX = 1099511627776.0;  // 2^40: fixed point of the grid masses
+static_assert(NGRID * 3 <= CHUNK_MAX / 2, "the grids reuse the count array");
+
+// The candidate bound from the chunks' histograms: bin j of chunk c holds the elements
+// j/8 .. (j+1)/8 log2-units below the chunk maximum xm_c, which lies o_c = (xmax - xm_c)
+// log2(e) / T below the row's. On a grid of bounds theta_g = -g/8 (log2-units of
+// exp(s - M)) the bins entirely above theta_g give lower bounds on the count and on the
+// mass of the elements above it; the bound is the highest theta_g whose lower bounds reach
+// k (top-k) or the top-p share of an upper bound on the normalizer with margins for the
+// reference's rounding (sample.rs:392-409). Every kept element lies above it.
+__device__ __forceinline__ float gather_bound(const KArgs& a, StreamSmem& sm, const RowCtx& C, float xmax,
+                                              double S_hi) {
+    const int tid = threadIdx.x;
+    const int nc = a.n_chunks;
+    uint32_t* CL = sm.hc;
+    uint64_t* ML = reinterpret_cast<uint64_t*>(sm.hc + NGRID);
+    for (int g = tid; g < NGRID; g += BLOCK) {
+        CL[g] = 0u;
+        ML[g] = 0ull;
+    }
+    __syncthreads();
+    const float eps = 0x1p-8f;
+    // the chunks' histograms, 16 words per thread in flight together
+    constexpr int PER = 16;
+    const uint32_t* vh = a.vhist + (int64_t)C.row * nc * HBINS;
+    for (int b0 = 0; b0 < nc * HBINS; b0 += PER * BLOCK) {
+        uint32_t hv[PER];
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            const int idx = b0 + r * BLOCK + tid;
+            hv[r] = (idx < nc * HBINS && (idx % HBINS) != HBINS - 1) ? ld_dev(vh + idx) : 0u;
+        }
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            const uint32_t cnt = hv[r];
+            if (!cnt) continue;
+            const int idx = b0 + r * BLOCK + tid;
+            const int c = idx / HBINS, j = idx % HBINS;
+            const float o = (xmax - sm.xm[c]) * C.rTl;
+            const float glo = ceilf(8.0f * o + (float)(j + 1) + 8.0f * eps);
+            if (glo < (float)NGRID) {
+                const int g = (int)glo;
+                lds_add(&CL[g], cnt);
+                const double m = (double)cnt * exp2(-(double)o - (double)(j + 1) / 8.0 - (double)eps);
+                lds_add64(&ML[g], (uint64_t)(m * MFIX));
+            }
+        }
+    }
+    __syncthreads();
+    // inclusive prefixes over the grid: thread t holds points PG*t .. PG*t + PG - 1
+    constexpr int PG = NGRID / BLOCK;
+    uint32_t cs = 0;
+    uint64_t ms = 0;
+#pragma unroll
+    for (int i = 0; i < PG; i++) {
+        cs += CL[tid * PG + i];
+        ms += ML[tid * PG + i];
+    }
+    uint32_t ct;
+    uint64_t mt;
+    uint32_t cpre = block_excl_scan<uint32_t>(cs, sm.wa, ct);
+    uint64_t mpre = block_excl_scan<uint64_t>(ms, reinterpret_cast<uint64_t*>(sm.ws), mt);
+    uint32_t gk = 0xFFFFFFFFu, gp = 0xFFFFFFFFu;
+    const double tgt = (double)fminf(C.top_p * 1.01f + 3e-4f, 2.0f) * S_hi * MFIX;
+#pragma unroll
+    for (int i = 0; i < PG; i++) {
+        cpre += CL[tid * PG + i];
+        mpre += ML[tid * PG + i];
+        const uint32_t g = (uint32_t)(tid * PG + i);
+        if (C.kmode && cpre >= (uint32_t)C.k) gk = min(gk, g);
+        if (C.pmode && (double)mpre >= tgt) gp = min(gp, g);
+    }
+    gk = block_min_u(gk, sm.wa);
+    gp = block_min_u(gp, sm.wa);
+    float th = -__builtin_inff();
+    if (C.kmode && gk != 0xFFFFFFFFu) th = fmaxf(th, -(float)gk / 8.0f);
+    if (C.pmode && gp != 0xFFFFFFFFu) th = fmaxf(th, -(float)gp / 8.0f);
+    return th;
+}
+
+// The row results from all chunks (the last workgroup of the row; every thread calls it).
+__device__ __forceinline__ void finish_row(const KArgs& a, StreamSmem& sm, int row) {
+    const RowCtx C = make_ctx(a, row);
+    const int tid = threadIdx.x;
+    const int nc = a.n_chunks;
+    static_assert(NCMAX <= BLOCK, "one chunk per thread");
+    ChunkPart P;
+    P.m = -__builtin_inff();
+    P.xm = -__builtin_inff();
+    P.raw_m = -__builtin_inff();
+    P.arg = P.raw_arg = 0xFFFFFFFFu;
+    P.sum = 0.0;
+    if (tid < nc) {
+        uint64_t* pp = reinterpret_cast<uint64_t*>(a.parts + (int64_t)row * nc + tid);
+        uint64_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = ld_dev64(pp + i);
+        P = __builtin_bit_cast(ChunkPart, w);
+        sm.xm[tid] = P.xm;
+    }
+    RowInfo R;
+    R.M = block_max(P.m, sm.wm);
+    R.xmax = block_max(P.xm, sm.wm);
+    R.gk = C.greedy ? block_max_u64(tid < nc ? argmax_key(P.m, P.arg) : 0ull, reinterpret_cast<uint64_t*>(sm.ws)) : 0ull;
+    R.rk = C.min_p > 1.0f ? block_max_u64(tid < nc ? argmax_key(P.raw_m, P.raw_arg) : 0ull,
+                                          reinterpret_cast<uint64_t*>(sm.ws))
+                          : 0ull;
+    R.th = __builtin_inff();
+    R.S_apx = 0.0f;
+    if (!C.greedy) {
+        const double mass = P.xm > -__builtin_inff() ? P.sum * exp2((double)((P.xm - R.xmax) * C.rTl)) : 0.0;
+        double tot;
+        const double pre = block_excl_scan<double>(mass, sm.ws, tot);
+        // the chunk maximum's term, from below: exactly 1 for the row maximum, else its
+        // estimate less the estimate's error (the roundings of x / T and of M)
+        float lb = 0.0f;
+        if (P.m == R.M) lb = 1.0f;
+        else if (P.xm > -__builtin_inff())
+            lb = exp2f((P.xm - R.xmax) * C.rTl) * (1.0f - 0x1p-12f - fabsf(R.M) * 0x1p-22f);
+        const float lbw = wave_scan_incl(lb, 0.0f, [](float u, float v) { return fmaxf(u, v); });
+        if (lane_id() == WAVE - 1) sm.wm[wave_id()] = lbw;
+        __syncthreads();
+        float lbx = __int_as_float(__shfl_up(__float_as_int(lbw), 1));  // the exclusive prefix maximum
+        lbx = lane_id() == 0 ? 0.0f : lbx;
+#pragma unroll
+        for (int w = 0; w < NWAVE; w++) lbx = w < wave_id() ? fmaxf(lbx, sm.wm[w]) : lbx;
+        __syncthreads();
+        if (tid < nc) a.qpre[(int64_t)row * nc + tid] = QPre{(float)pre, fmaxf(lbx, 0.0f)};
+        R.S_apx = (float)tot;
+        const bool list_mode = C.kmode || C.pmode || C.mmode;
+        float th = -__builtin_inff();
+        if ((C.kmode || C.pmode) && !C.pen_hash && R.xmax > -__builtin_inff())
+            th = gather_bound(a, sm, C, R.xmax, tot * (1.0 + 1e-4));
+        if (C.mmode) th = fmaxf(th, log2f(C.min_p) - 0x1p-6f);
+        if (list_mode) R.th = th;
+    }
+    if (tid == 0) {
+        a.rinfo[row] = R;
+        a.rowcnt[row] = 0u;
+        a.arrive[row] = 0u;
+    }
+}
 
 template <bool BF16, int VEC, bool FULL>
 __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int row, int chunk, uint32_t c0,
@@ -229,8 +379,8 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
         part.xm = lm;
     }
     if (want_hist) {
-        // bin j: the element lies j/8 .. (j+1)/8 log2-units below the chunk maximum (the
-        // last bin takes everything further down); masked elements are not counted
+        // bin j: the element lies j/8 .. (j+1)/8 log2-units below the chunk maximum; the
+        // elements further down (most of them) and the masked ones are not counted
         if (lm > -__builtin_inff()) {
             const float sc = C.rTl * (float)HBIN_PER_LOG2;
 #pragma unroll
@@ -238,18 +388,31 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
 #pragma unroll
                 for (int e = 0; e < EPV; e++) {
                     const float xv = x[q][e];
-                    if (xv > -__builtin_inff()) {
-                        const float f = (lm - xv) * sc;
-                        const uint32_t j = f < (float)(HBINS - 1) ? (uint32_t)f : (uint32_t)(HBINS - 1);
-                        lds_add(&sm.hc[j], 1u);
-                    }
+                    const float f = (lm - xv) * sc;
+                    if (f < (float)(HBINS - 1)) lds_add(&sm.hc[(uint32_t)f], 1u);
                 }
         }
         __syncthreads();
         uint32_t* dst = a.vhist + ((int64_t)row * a.n_chunks + chunk) * HBINS;
-        for (int i = tid; i < HBINS; i += BLOCK) dst[i] = sm.hc[i];
+        for (int i = tid; i < HBINS; i += BLOCK) st_dev(dst + i, sm.hc[i]);
     }
-    if (tid == 0) a.parts[(int64_t)row * a.n_chunks + chunk] = part;
+    if (tid < 4) {
+        const uint64_t* pw = reinterpret_cast<const uint64_t*>(&part);
+        uint64_t v = pw[0];
+#pragma unroll
+        for (int i = 1; i < 4; i++) v = tid == i ? pw[i] : v;
+        st_dev64(reinterpret_cast<uint64_t*>(a.parts + (int64_t)row * a.n_chunks + chunk) + tid, v);
+    }
+    // the last chunk of the row to arrive finishes it: the chunk results go out with
+    // device-coherent stores, each wave waits for its own before the count, and the finisher
+    // reads them from the coherence point (no cache writeback or invalidation, which would
+    // cost every workgroup and evict the logits the others stream)
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (tid == 0) sm.last = glb_add(&a.arrive[row], 1u) == (uint32_t)(a.n_chunks - 1) ? 1u : 0u;
+    __syncthreads();
+    if (!sm.last) return;
+    finish_row(a, sm, row);
 }
 
 // ---- launch ----------------------------------------------------------------------------

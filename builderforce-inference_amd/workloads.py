@@ -9,6 +9,8 @@ finishes in seconds; everything else keeps the configuration's shape and distrib
   C2  B=64,  V=151936 f32 ~N(0,2.5) + 1..16 peaked ids (+6..+12); per-row T U[0.2,1.5],
       k in {0,20,50,100}, p U[0.8,1.0], min-p 0.05; 512-id Zipf(1.1) histories with
       repetition 1.1, presence 0.5, frequency 0.3
+  C2M C2 under C3's grammar allow-masks (the full-feature row: penalties, top-k/top-p/min-p
+      and a mask)
   C3  B=32,  V=151936 f32 as C2 logits, packed allow-mask with allowed fraction
       log-uniform in [0.1%, 30%] in runs of 1..64 ids (some rows allow exactly 1 id);
       T 1.0 / p 0.9
@@ -84,7 +86,7 @@ def run_masks(rng, B, V, frac=(0.001, 0.30), runs=(1, 64), single_rows=(0,)):
 
 
 def config(name: str, seed: int = 0, scale_v: float = 1.0, greedy: bool = False) -> dict:
-    rng = np.random.default_rng([seed, {"C1": 1, "C2": 2, "C3": 3, "C4": 4, "C5": 5}[name]])
+    rng = np.random.default_rng([seed, {"C1": 1, "C2": 2, "C3": 3, "C4": 4, "C5": 5, "C2M": 6}[name]])
     out = dict(name=name, mask=None, dtype="f32")
     if name == "C1":
         V = max(int(QWEN3_V * scale_v), 64)
@@ -95,7 +97,7 @@ def config(name: str, seed: int = 0, scale_v: float = 1.0, greedy: bool = False)
         off = np.array([0, 64], np.int64)
         p = dict(temperature=0.0 if greedy else 0.7, top_k=40, top_p=0.95, repeat_penalty=1.1)
         params = params_array([p])
-    elif name == "C2":
+    elif name in ("C2", "C2M"):
         V = max(int(QWEN3_V * scale_v), 256)
         B = 64
         x = peaked_logits(rng, B, V)
@@ -112,6 +114,8 @@ def config(name: str, seed: int = 0, scale_v: float = 1.0, greedy: bool = False)
                 frequency_penalty=0.3,
             ))
         params = params_array(rows)
+        if name == "C2M":  # the same rows under a grammar allow-mask (C3's masks)
+            out["mask"] = run_masks(rng, B, V, single_rows=(0, 7))
     elif name == "C3":
         V = max(int(QWEN3_V * scale_v), 256)
         B = 32

@@ -80,18 +80,19 @@ const char *bfi_smp_last_error(const bfi_smp_ctx *ctx);
 int bfi_smp_abi_version(void);
 
 /* Profiling (no counterpart in the reference; for benchmarks): while enabled, every launch
- * times its two kernels (the streaming pass over the logits, then the per-row selection)
- * with start/stop HIP events recorded in the kernels' own dispatch packets on the caller's
- * stream, so launch gaps are excluded. Profiling may be switched on for some launches only;
- * the record keeps them until bfi_smp_profile waits for them, returns the summed kernel
- * times in ms and clears it (at most 65536 launches). */
+ * times its three kernels (the streaming pass over the logits, the quantizing pass, the
+ * per-row pass) with start/stop HIP events recorded in the kernels' own dispatch packets on
+ * the caller's stream. Profiling may be switched on for some launches only; the record
+ * keeps them until bfi_smp_profile waits for them, writes the summed times in ms to
+ * kernel_ms[0..3] (k_stream, k_quant, k_row, and the whole call from k_stream's start to
+ * k_row's end, gaps included) and clears it (at most 65536 launches). */
 int bfi_smp_set_profiling(bfi_smp_ctx *ctx, int enabled);
-int bfi_smp_profile(bfi_smp_ctx *ctx, double *stream_ms, double *select_ms, int64_t *launches);
+int bfi_smp_profile(bfi_smp_ctx *ctx, double *kernel_ms, int64_t *launches);
 
 /* Phase trace (diagnostics, no counterpart in the reference): while enabled, each launch
  * records wall-clock (100 MHz) timestamps at phase boundaries of every workgroup into a
  * context buffer: 8 words per streaming workgroup (row-major by row, chunk), then 16 per
- * row for its selection workgroup.
+ * row for its row-pass workgroup.
  * bfi_smp_trace copies the last launch's record (synchronous) and returns the word count. */
 int bfi_smp_set_tracing(bfi_smp_ctx *ctx, int enabled);
 int64_t bfi_smp_trace(bfi_smp_ctx *ctx, uint64_t *out, int64_t max_words);
