@@ -103,6 +103,9 @@ bool choose_shape(int64_t n_rows, int64_t V, int bf16, Shape& s) {
     return found;
 }
 
+// Window elements a chunk may list (beyond: it is streamed exactly).
+size_t qcap_of(const Shape& s) { return (size_t)(s.chunk < bfi::QWIN ? s.chunk : bfi::QWIN); }
+
 struct Layout {
     size_t parts, vhist, row_res, row_pen, spill, rinfo, qpre, qhead, qitem, rowcnt, total;
 };
@@ -127,7 +130,7 @@ Layout layout(int64_t n_rows, int64_t V, const Shape& s, int bm_words) {
     L.qhead = off;
     off = align_up(off + (size_t)n_rows * s.n_chunks * sizeof(bfi::QHead), 256);
     L.qitem = off;
-    off = align_up(off + (size_t)n_rows * s.n_chunks * (bfi::QWIN + 1) * sizeof(bfi::QItem), 256);
+    off = align_up(off + (size_t)n_rows * s.n_chunks * (qcap_of(s) + 1) * sizeof(bfi::QItem), 256);
     L.rowcnt = off;
     off = align_up(off + (size_t)n_rows * sizeof(uint32_t), 256);
     L.total = off;
@@ -278,6 +281,7 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     a.arrive = ctx->ctr;
     a.seq_ctr = ctx->ctr + c.n_rows;
     a.bm_words = bm_words;
+    a.qcap = (int32_t)qcap_of(s);
     a.trace = nullptr;
     if (ctx->tracing) {
         size_t words = (size_t)c.n_rows * s.n_chunks * 8 + (size_t)c.n_rows * 16;

@@ -67,7 +67,7 @@ struct QPre {
 // by "window" elements, whose binade or rounding the pass could not settle: those near a
 // binade boundary of the predicted running sum, and ties. Item k holds window element k
 // with its exact exp(s - M) and the run before it; the last item holds the tail run.
-constexpr int QWIN = 4096;          // window elements per chunk (beyond: the chunk is exact)
+constexpr int QWIN = 4096;          // window elements per chunk at most (beyond: the chunk is exact)
 constexpr uint32_t QF_EXACT = 1u;   // the row kernel streams this chunk exactly
 constexpr uint32_t QI_NONE = 0xFFFFFFFFu;  // item id of the tail run (no element)
 struct QItem {
@@ -124,11 +124,11 @@ struct KArgs {
     RowInfo* rinfo;      // per row: the streaming pass's row results
     QPre* qpre;          // per (row, chunk): the running sum's prediction at the chunk's start
     QHead* qhead;        // per (row, chunk): the quantizing pass's summary
-    QItem* qitem;        // per (row, chunk): QWIN + 1 items
+    QItem* qitem;        // per (row, chunk): qcap + 1 items
     uint32_t* arrive;    // per row: chunks done (the last one finishes the row; kept zero)
     uint32_t* rowcnt;    // per row: candidates gathered by the quantizing pass
     int32_t bm_words;
-    int32_t pad1;
+    int32_t qcap;        // window elements a chunk lists: min(QWIN, chunk)
     uint64_t* trace;     // optional phase timestamps (wall clock) per workgroup
 };
 

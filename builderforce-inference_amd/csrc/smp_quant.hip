@@ -158,7 +158,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
     const float Pc = ld_uniform(&a.qpre[rc].P);
     const float Lc = ld_uniform(&a.qpre[rc].lb);
     QHead* const head = a.qhead + rc;
-    QItem* const items = a.qitem + rc * (QWIN + 1);
+    QItem* const items = a.qitem + rc * (a.qcap + 1);
     const float Kc = -(M * 1.44269504088896341f);
     // candidates: (x / T - M) log2(e) estimated as x * rTl + Kc, above the bound less the
     // estimate's error (the roundings of x / T, of M and of the products, in log2-units)
@@ -378,7 +378,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             }
             nwin = run;
         }
-        uint32_t flags = nwin > (uint32_t)QWIN ? QF_EXACT : 0u;
+        uint32_t flags = nwin > (uint32_t)a.qcap ? QF_EXACT : 0u;
         uint32_t bad = 0;
         if (!flags) {
             // the windows' (index, x) into their items (the exact values come below), the run

@@ -1325,12 +1325,13 @@ struct ChainIO {
 
 // Walks the items from io.next until all are done (lo == hi) or a range must be re-streamed.
 // Every thread calls it.
-__device__ __forceinline__ ChainIO chain_walk(const QItem* items, int32_t nc, uint32_t chunk, uint32_t V,
+__device__ __forceinline__ ChainIO chain_walk(const QItem* items, uint32_t qstride, int32_t nc, uint32_t chunk, uint32_t V,
                                            uint32_t total, ChainIO io, uint64_t* tr) {
     RowSmem& sm = g_sm;
     const int tid = threadIdx.x;
     QItem* const stage = reinterpret_cast<QItem*>(sm.grp);
     items = rflp(items);
+    qstride = (uint32_t)rfli((int32_t)qstride);
     tr = rflp(tr);
     nc = rfli(nc);
     chunk = (uint32_t)rfli((int32_t)chunk);
@@ -1356,7 +1357,7 @@ __device__ __forceinline__ ChainIO chain_walk(const QItem* items, int32_t nc, ui
                     v[r] = QItem{QI_EXACT, 0.0f, 0u, (int32_t)(((uint32_t)c << 16))};
                 } else {
                     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-                    const u32x4 it = *(const BFI_GLB u32x4*)(items + (int64_t)c * (QWIN + 1) + (base + g - sm.coff[c]));
+                    const u32x4 it = *(const BFI_GLB u32x4*)(items + (int64_t)c * qstride + (base + g - sm.coff[c]));
                     v[r] = QItem{it.x, __uint_as_float(it.y), it.z, (int32_t)(((uint32_t)c << 16) | (it.w & 0xFFFFu))};
                 }
             }
@@ -1558,7 +1559,8 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
         ChainIO io{0.0f, 0u, 0u, 0u};
         uint32_t nfb = 0;
         for (;;) {
-            io = chain_walk(a.qitem + (int64_t)row * nc * (QWIN + 1), nc, (uint32_t)a.chunk, V, total, io,
+            io = chain_walk(a.qitem + (int64_t)row * nc * (a.qcap + 1), (uint32_t)(a.qcap + 1), nc,
+                            (uint32_t)a.chunk, V, total, io,
                             a.trace ? a.trace + (int64_t)a.n_rows * nc * 8 + (int64_t)row * 16 : nullptr);
             if (io.hi <= io.lo) {
                 if (io.next >= total) break;
