@@ -61,6 +61,7 @@ def lib():
         L.bfi_smp_set_profiling.argtypes = [P, I32]
         L.bfi_smp_profile.argtypes = [P, P, P]
         L.bfi_smp_sample_rows.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P]
+        L.bfi_smp_sample_rows_noalloc.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P]
         L.bfi_smp_target_rows.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P, P, P, P, P, I64, P, P]
         L.bfi_smp_verify.argtypes = [P, P, I32, I64, I64, I64, I64, P, P, P, P, P, P, I64, P, P, P, P, P]
         L.bfi_smp_sample_host.argtypes = [P, P, I64, P, I64, P, P, ctypes.c_float, P]
@@ -243,6 +244,20 @@ class Sampler:
                                          _dptr(hist), _dptr(hist_off), _dptr(mask), ms, _dptr(u), _dptr(out),
                                          self._stream(stream))
         self._check(rc, "bfi_smp_sample_rows")
+        return out
+
+    def sample_rows_noalloc(self, logits, params, u, out, hist=None, hist_off=None, mask=None, stream=None):
+        """sample_rows in the library's fixed per-device workspace (bfi_smp_sample_rows_noalloc:
+        no device allocation; calls that overlap on one GPU race)."""
+        import torch
+
+        B, V = logits.shape
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        ms = 0 if mask is None else mask.stride(0)
+        rc = self._L.bfi_smp_sample_rows_noalloc(self._ctx, _dptr(logits), dtype, B, V, logits.stride(0),
+                                                 _dptr(params), _dptr(hist), _dptr(hist_off), _dptr(mask), ms,
+                                                 _dptr(u), _dptr(out), self._stream(stream))
+        self._check(rc, "bfi_smp_sample_rows_noalloc")
         return out
 
     def target_rows(self, logits, params, u, cap, hist=None, hist_off=None, mask=None, stream=None):

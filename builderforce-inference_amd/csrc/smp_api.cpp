@@ -12,7 +12,46 @@
 #include "../../include/bfi_sampler.h"
 #include "smp_device.h"
 
+#include <mutex>
 #include <vector>
+
+// ---- the allocation-free entry point's workspace ---------------------------------------
+//
+// bfi_smp_sample_rows_noalloc runs the same kernels in a fixed device array instead of the
+// context's allocated workspace (for callers that cannot allocate: graph capture, serving
+// loops). Each device holds its own copy of the array from the library's load until the
+// process ends; its address on a device comes from hipGetSymbolAddress (the array's name in
+// host code is only a stand-in). Every call on a device shares it.
+static __device__ __align__(256) unsigned char scratch[BFI_SMP_NOALLOC_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES];  // per device: the array's device address (null: not yet)
+
+// Resolves the array's address on `device` (the current device) once; 0 on success.
+hipError_t scratch_setup(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return hipSuccess;
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = ptr;
+    return hipSuccess;
+}
+void* scratch_ptr(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return device >= 0 && device < MAX_DEVICES ? g_scratch_ptr[device] : nullptr;
+}
+
+// Zero-fill of counters that must start at zero (a kernel, not a memset: callers may capture
+// the call into a graph).
+__global__ void k_fill_zero(uint32_t* p, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+}  // namespace
 
 namespace bfi {
 hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
@@ -194,7 +233,13 @@ struct Call {
     uint32_t* out_next = nullptr;
 };
 
-int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
+// A workspace the caller provides (the allocation-free entry point): base and capacity.
+struct Fixed {
+    char* base;
+    size_t cap;
+};
+
+int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream, const Fixed* fixed = nullptr) {
     if (c.dtype != BFI_SMP_F32 && c.dtype != BFI_SMP_BF16)
         return fail(ctx, BFI_SMP_EINVAL, "dtype %d is not BFI_SMP_F32 or BFI_SMP_BF16", c.dtype);
     if (c.n_rows < 0 || c.V < 0) return fail(ctx, BFI_SMP_EINVAL, "negative n_rows or n_vocab");
@@ -234,8 +279,29 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
         return fail(ctx, BFI_SMP_EINVAL, "no launch shape for n_vocab %lld", (long long)c.V);
     const Layout L = layout(c.n_rows, c.V, s, bm_words);
     const size_t ctr_words = (size_t)c.n_rows + (verify ? (size_t)c.n_seq : 0);
-    int rc = ensure_ws(ctx, L.total, ctr_words, stream);
-    if (rc) return rc;
+    char* ws = nullptr;
+    uint32_t* ctr = nullptr;
+    if (fixed) {
+        const size_t need = L.total + align_up(ctr_words * sizeof(uint32_t), 256);
+        if (need > fixed->cap)
+            return fail(ctx, BFI_SMP_EINVAL,
+                        "%lld rows of %lld logits need %zu bytes of workspace; the allocation-free entry point "
+                        "holds %zu (BFI_SMP_NOALLOC_BYTES)",
+                        (long long)c.n_rows, (long long)c.V, need, fixed->cap);
+        ws = fixed->base;
+        ctr = (uint32_t*)(fixed->base + L.total);
+        // the counters start at zero (the kernels leave them so, but an earlier call may have
+        // failed midway)
+        const uint32_t n = (uint32_t)ctr_words;
+        hipLaunchKernelGGL(k_fill_zero, dim3((n + 255) / 256), dim3(256), 0, stream, ctr, n);
+        hipError_t e0 = hipGetLastError();
+        if (e0 != hipSuccess) return hip_fail(ctx, e0, "counter fill launch");
+    } else {
+        int rc = ensure_ws(ctx, L.total, ctr_words, stream);
+        if (rc) return rc;
+        ws = ctx->ws;
+        ctr = ctx->ctr;
+    }
 
     bfi::KArgs a;
     memset(&a, 0, sizeof a);
@@ -268,22 +334,22 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     a.u_bonus = c.u_bonus;
     a.out_accepted = c.out_acc;
     a.out_next = c.out_next;
-    a.parts = (bfi::ChunkPart*)(ctx->ws + L.parts);
-    a.vhist = (uint32_t*)(ctx->ws + L.vhist);
-    a.row_res = (uint32_t*)(ctx->ws + L.row_res);
-    a.row_pen = (uint32_t*)(ctx->ws + L.row_pen);
-    a.spill = (uint64_t*)(ctx->ws + L.spill);
-    a.rinfo = (bfi::RowInfo*)(ctx->ws + L.rinfo);
-    a.qpre = (bfi::QPre*)(ctx->ws + L.qpre);
-    a.qhead = (bfi::QHead*)(ctx->ws + L.qhead);
-    a.qitem = (bfi::QItem*)(ctx->ws + L.qitem);
-    a.rowcnt = (uint32_t*)(ctx->ws + L.rowcnt);
-    a.arrive = ctx->ctr;
-    a.seq_ctr = ctx->ctr + c.n_rows;
+    a.parts = (bfi::ChunkPart*)(ws + L.parts);
+    a.vhist = (uint32_t*)(ws + L.vhist);
+    a.row_res = (uint32_t*)(ws + L.row_res);
+    a.row_pen = (uint32_t*)(ws + L.row_pen);
+    a.spill = (uint64_t*)(ws + L.spill);
+    a.rinfo = (bfi::RowInfo*)(ws + L.rinfo);
+    a.qpre = (bfi::QPre*)(ws + L.qpre);
+    a.qhead = (bfi::QHead*)(ws + L.qhead);
+    a.qitem = (bfi::QItem*)(ws + L.qitem);
+    a.rowcnt = (uint32_t*)(ws + L.rowcnt);
+    a.arrive = ctr;
+    a.seq_ctr = ctr + c.n_rows;
     a.bm_words = bm_words;
     a.qcap = (int32_t)qcap_of(s);
     a.trace = nullptr;
-    if (ctx->tracing) {
+    if (ctx->tracing && !fixed) {
         size_t words = (size_t)c.n_rows * s.n_chunks * 8 + (size_t)c.n_rows * 16;
         if (words > ctx->trace_words) {
             if (ctx->trace) (void)hipFree(ctx->trace);
@@ -300,7 +366,7 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream) {
     }
 
     hipEvent_t ev[EV_PER_LAUNCH] = {};
-    if (ctx->profiling) {
+    if (ctx->profiling && !fixed) {
         if (ctx->ev_used + EV_PER_LAUNCH > ctx->ev_pool.size()) {
             if (ctx->ev_pool.size() >= EV_PER_LAUNCH * 65536)
                 return fail(ctx, BFI_SMP_EINVAL, "profiling record full: read it");
@@ -345,6 +411,12 @@ int bfi_smp_create(int device, bfi_smp_ctx** out) {
     if (g.err != hipSuccess) {
         delete ctx;
         return fail(nullptr, BFI_SMP_EHIP, "hipSetDevice(%d): %s", device, hipGetErrorString(g.err));
+    }
+    // the allocation-free entry point's array on this device (once per device)
+    if ((e = scratch_setup(device)) != hipSuccess) {
+        delete ctx;
+        return fail(nullptr, BFI_SMP_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                    hipGetErrorString(e));
     }
     *out = ctx;
     return BFI_SMP_OK;
@@ -428,6 +500,30 @@ int bfi_smp_sample_rows(bfi_smp_ctx* ctx, const void* d_logits, int dtype, int64
     c.u = d_u;
     c.out = d_out;
     return run(ctx, c, (hipStream_t)stream);
+}
+
+int bfi_smp_sample_rows_noalloc(bfi_smp_ctx* ctx, const void* d_logits, int dtype, int64_t n_rows, int64_t n_vocab,
+                                int64_t row_stride, const bfi_smp_row_params* d_params, const uint32_t* d_hist,
+                                const int64_t* d_hist_off, const uint32_t* d_mask, int64_t mask_stride,
+                                const float* d_u, uint32_t* d_out, void* stream) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    void* ptr = scratch_ptr(ctx->device);
+    if (!ptr) return fail(ctx, BFI_SMP_EHIP, "the fixed workspace of device %d is not set up", ctx->device);
+    Call c{};
+    c.logits = d_logits;
+    c.dtype = dtype;
+    c.n_rows = n_rows;
+    c.V = n_vocab;
+    c.row_stride = row_stride;
+    c.params = d_params;
+    c.hist = d_hist;
+    c.hist_off = d_hist_off;
+    c.mask = d_mask;
+    c.mask_stride = mask_stride;
+    c.u = d_u;
+    c.out = d_out;
+    const Fixed f{(char*)ptr, (size_t)BFI_SMP_NOALLOC_BYTES};
+    return run(ctx, c, (hipStream_t)stream, &f);
 }
 
 int bfi_smp_target_rows(bfi_smp_ctx* ctx, const void* d_logits, int dtype, int64_t n_rows, int64_t n_vocab,

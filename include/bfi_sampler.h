@@ -120,6 +120,24 @@ int bfi_smp_sample_rows(bfi_smp_ctx *ctx, const void *d_logits, int dtype, int64
                         int64_t mask_stride, const float *d_u, uint32_t *d_out, void *stream);
 
 /*
+ * bfi_smp_sample_rows without any allocation: no counterpart in the reference; for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and results as bfi_smp_sample_rows, but
+ * the kernels' workspace is a fixed array of BFI_SMP_NOALLOC_BYTES per device, which the
+ * library holds from its load until the process ends (its address is resolved once per
+ * device by bfi_smp_create). A call whose rows need more workspace than that fails with
+ * BFI_SMP_EINVAL and a message naming both sizes (8 rows at n_vocab = 151936, or 64
+ * rows at n_vocab = 16384). Every call on a device shares the one array: calls that overlap
+ * on one GPU (other streams, other contexts, other threads) race, so the caller orders them.
+ * Profiling and tracing records are not kept for these calls.
+ */
+#define BFI_SMP_NOALLOC_BYTES (64u << 20)
+int bfi_smp_sample_rows_noalloc(bfi_smp_ctx *ctx, const void *d_logits, int dtype, int64_t n_rows,
+                                int64_t n_vocab, int64_t row_stride, const bfi_smp_row_params *d_params,
+                                const uint32_t *d_hist, const int64_t *d_hist_off, const uint32_t *d_mask,
+                                int64_t mask_stride, const float *d_u, uint32_t *d_out, void *stream);
+
+/*
  * The distribution `sample` draws from, per row (sample.rs:326-427 `target()`), plus the
  * drawn token. For each row b:
  *   d_kind[b]      BFI_SMP_TARGET_TOKEN (greedy / min-p fallback) or _WEIGHTS
