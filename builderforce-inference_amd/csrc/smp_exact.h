@@ -41,6 +41,29 @@ __constant__ const uint64_t EXP2_32[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
+// glibc's main path for x in [-103.97, 88.72]: 2^(k/32) from the table `tab` (EXP2_32, or a
+// copy of it in LDS) times the cubic in r, in double precision with FMA, rounded to float.
+__device__ __forceinline__ float expf_core(float x, const uint64_t* tab) {
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    const double SHIFT = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    double kd = __builtin_fma(InvLn2N, xd, SHIFT);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= SHIFT;
+    const double r = __builtin_fma(InvLn2N, xd, -kd);
+    const uint64_t t = tab[ki & 31u] + (ki << 47);
+    const double s = __longlong_as_double((long long)t);
+    const double z = __builtin_fma(C0, r, C1);
+    const double r2 = r * r;
+    double y = __builtin_fma(C2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
 // expf(x) exactly as glibc returns it. Table entry by a per-lane index: read from the
 // constant table through a generic load (it stays in the scalar/vector caches).
 __device__ __forceinline__ float expf_ref(float x) {
@@ -52,24 +75,17 @@ __device__ __forceinline__ float expf_ref(float x) {
         if (x > 0x1.62e42ep6f) return __builtin_inff();
         if (x < -0x1.9fe368p6f) return 0.0f;
     }
-    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
-    const double SHIFT = 0x1.8p+52;
-    const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
-    const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
-    const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-    const double xd = (double)x;
-    double kd = __builtin_fma(InvLn2N, xd, SHIFT);
-    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
-    kd -= SHIFT;
-    const double r = __builtin_fma(InvLn2N, xd, -kd);
-    const uint64_t t = EXP2_32[ki & 31u] + (ki << 47);
-    const double s = __longlong_as_double((long long)t);
-    const double z = __builtin_fma(C0, r, C1);
-    const double r2 = r * r;
-    double y = __builtin_fma(C2, r, 1.0);
-    y = __builtin_fma(z, r2, y);
-    y = y * s;
-    return (float)y;
+    return expf_core(x, EXP2_32);
+}
+
+// expf(x) for x <= 0 as glibc returns it, without branches: below its underflow bound
+// (-0x1.9fe368p6, where glibc returns 0), at -inf and at NaN (a masked element's x) the
+// result is 0; every other x takes glibc's main path. The main path runs for every x (its
+// table index is masked to 0..31, so any input is safe) and the selection discards its
+// value outside the range. `tab`: EXP2_32 or a copy in LDS.
+__device__ __forceinline__ float expf_nonpos(float x, const uint64_t* tab) {
+    const float y = expf_core(x, tab);
+    return x >= -0x1.9fe368p6f ? y : 0.0f;
 }
 
 // ---- sequential f32 sums by binades -------------------------------------------------------

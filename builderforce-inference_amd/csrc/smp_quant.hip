@@ -3,24 +3,24 @@
 //
 // The reference's normalizer is a sequential f32 sum over the row (sample.rs:381-386). While
 // the running sum stays inside one binade [2^k, 2^(k+1)), each addition moves it by a whole
-// number of units u = 2^(k-23): RN(e / u) (smp_exact.h). From the row maximum M and the
-// approximate normalizer mass before this chunk (both from the streaming pass's row
-// finisher), a workgroup predicts the running sum before each of its elements, and so the
-// binade each addition lands in. The prediction is an interval: the estimated prefix
-// widened by QEPS relative both ways (several times the f32 sum's largest drift from the
-// exact one on the benchmark rows), raised to the largest term added so far (the f32 sum
-// never falls below any of its terms). An element is "certain" when the interval before its
-// addition and the one after lie in one binade; its units are then RN(e / u) at that
-// binade, exactly (a precise estimate, or glibc's expf where the estimate lies near a
-// rounding boundary). The others ("windows": near a binade boundary, the row's first
-// terms, ties) are listed with their exact exp(s - M). In index order, the certain elements
-// between two windows all lie in one binade (the intervals never decrease, so a change of
-// binade needs an interval that straddles the boundary: a window), and the pass sums them
-// per gap as a run. The row kernel chains the chunks: it adds a run in one step after
-// checking that the actual running sum lies in the run's binade and stays there, and walks
-// the windows exactly; a failed check re-streams the rest of the chunk exactly, so a wrong
-// prediction costs time, never the result. On the way the pass gathers the candidates of
-// the kept set into the row's list.
+// number of units u = 2^(k-23): RN(e / u) (smp_exact.h). The pass computes every term
+// e = expf(fl(x / T) - M) exactly as the reference does (glibc's expf in double precision,
+// full rate on CDNA's VALU). From the row maximum M and the approximate normalizer mass
+// before this chunk (both from the streaming pass's row finisher), a workgroup predicts the
+// running sum before each of its elements, and so the binade each addition lands in. The
+// prediction is an interval: the prefix of the exact terms widened by QEPS relative both
+// ways (several times the f32 sum's largest drift from the exact one on the benchmark rows),
+// raised to the largest term added so far (the f32 sum never falls below any of its terms).
+// An element is "certain" when the interval before its addition and the one after lie in
+// one binade; its units are then RN(e / u) at that binade, exactly. The others ("windows":
+// near a binade boundary, ties, terms of 2^23 units or more) are listed with their exact e.
+// In index order, the certain elements between two windows all lie in one binade (the
+// intervals never decrease, so a change of binade needs an interval that straddles the
+// boundary: a window), and the pass sums them per gap as a run. The row kernel chains the
+// chunks: it adds a run in one step after checking that the actual running sum lies in the
+// run's binade and stays there, and walks the windows exactly; a failed check re-streams
+// the rest of the chunk exactly, so a wrong prediction costs time, never the result. On the
+// way the pass gathers the candidates of the kept set into the row's list.
 #include <hip/hip_ext.h>
 
 #define BFI_BLOCK 512
@@ -31,42 +31,44 @@
 namespace bfi {
 
 constexpr float QEPS = 0x1p-9f;   // relative width of the running-sum prediction
-constexpr float RHO0 = 0x1p-19f;  // relative error bound of the precise exp estimate
-constexpr float L2E_HI = 1.44269502162933349609375f;  // fl(log2(e))
-constexpr float L2E_LO = 1.925963033500011079e-8f;    // log2(e) - L2E_HI
-constexpr float LN2_F = 0.693147180559945309f;
 constexpr uint32_t UE_BIAS = 1024u;
 constexpr int QVMAX = 4;             // 16-byte vectors per thread
+constexpr int NSLOT = QVMAX * NWAVE;  // (vector, wave) slots of a chunk, in index order
 
 struct __align__(16) QuantSmem {
+    uint64_t etab[32];       // glibc's expf table (EXP2_32), per-lane reads from LDS
     uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids (two 16-bit halves a word)
     uint32_t rq[QWIN + 1];   // per run: units
     uint32_t rhi[QWIN + 1];  // per run: its unit exponent + 150 (0: no element)
-    float vs[QVMAX][NWAVE];  // per vector, per wave: sums of the estimates
-    float vm[QVMAX][NWAVE];  // per vector, per wave: largest term (lower bound)
-    uint32_t vc[QVMAX][NWAVE];  // per vector, per wave: window counts
+    float vs[NSLOT];         // per (vector, wave): sum of the terms
+    float vm[NSLOT];         // per (vector, wave): largest term (the running sum's lower bound)
+    uint32_t vc[NSLOT];      // per (vector, wave): window count
     uint32_t wg[NWAVE];
     uint32_t wb[NWAVE];
     uint32_t gbase;
 };
+static_assert(NSLOT <= WAVE, "one lane per (vector, wave) slot");
 
 __device__ __forceinline__ uint32_t lds_min(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_min((BFI_LDS uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// exp(fl(x / T) - M) exactly as the reference rounds it (sample.rs:374, 383); out of line:
-// glibc's expf should exist once in the kernel's code.
-__device__ __noinline__ float quant_exact(float x, float T, float rT, int32_t fast_div, float M) {
-    float s;
-    const uint32_t ax = __float_as_uint(x) & 0x7FFFFFFFu;
-    if (fast_div && !((ax - 1u < 0x0D7FFFFFu) || (ax - 0x71800000u < 0x0E000000u))) {
-        const float q = x * rT;
-        const float er = __builtin_fmaf(-q, T, x);
-        s = er != er ? q : __builtin_fmaf(er, rT, q);
-    } else {
-        s = x / T;
+// The exclusive prefixes (sum and maximum), over the chunk's (vector, wave) slots in index
+// order, of the per-slot values vs and vm, at this wave's slot of each vector (wave-uniform).
+template <int QV>
+__device__ __forceinline__ void slot_prefix(const float* vs, const float* vm, int w, float (&pre)[QV],
+                                            float (&pmax)[QV]) {
+    const int lane = lane_id();
+    const float tv = lane < QV * NWAVE ? vs[lane] : 0.0f;
+    const float tm = lane < QV * NWAVE ? vm[lane] : 0.0f;
+    const float ts = wave_excl_of_incl(wave_scan_incl(tv, 0.0f, [](float u, float v) { return u + v; }), 0.0f);
+    const float tx =
+        wave_excl_of_incl(wave_scan_incl(tm, 0.0f, [](float u, float v) { return fmaxf(u, v); }), 0.0f);
+#pragma unroll
+    for (int q = 0; q < QV; q++) {
+        pre[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ts), q * NWAVE + w));
+        pmax[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tx), q * NWAVE + w));
     }
-    return expf_ref(s - M);
 }
 
 template <bool BF16, int QV, bool FULL>
@@ -74,7 +76,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                                             uint32_t c1);
 
 template <bool BF16, int QV>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4))) void k_quant(KArgs a) {  // 2 workgroups per CU
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void k_quant(KArgs a) {  // 3 workgroups per CU
     __shared__ QuantSmem sm;
     const uint32_t G = gridDim.x, bid = blockIdx.x;
     const uint32_t q8 = G / 8, r8 = G % 8, xcd = bid % 8, slot = bid / 8;
@@ -91,37 +93,32 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4))) void
         quant_chunk<BF16, QV, false>(a, sm, row, chunk, c0, c1);
 }
 
-// The units RN(e / 2^ue) of one element (ue = elo - 150) from the precise estimate: s =
-// fl(x / T) exactly (Markstein's corrected quotient, for |x| in [2^-100, 2^100) and T in
-// [2^-20, 2^20]), d = fl(s - M) as the reference rounds it, exp(d) = 2^(h + l) with
-// h = fl(d log2(e)) and l its rounding error plus log2(e)'s own, as exp2(h) (1 + l ln 2),
-// within RHO0 of glibc's expf(d); below 2^-120, 2^(h - ue) directly with its exponent's
-// rounding added to the bound. `sure`: the estimate lies far enough from a rounding
-// boundary (else the element is a window and its exact value decides). Straight-line.
-__device__ __forceinline__ uint32_t elem_units(float xv, uint32_t elo, bool fdiv, float T, float rT, float M,
-                                               bool& sure) {
-    const int32_t ue = (int32_t)elo - 150;
-    const uint32_t ax = __float_as_uint(xv) & 0x7FFFFFFFu;
-    const bool dok = fdiv & (((ax - 0x0D800000u) < 0x64000000u) | (ax == 0u));
-    const float q0 = xv * rT;
-    const float r0 = __builtin_fmaf(-q0, T, xv);
-    const float d = __builtin_fmaf(r0, rT, q0) - M;
-    const float h = d * L2E_HI;
-    const float l = __builtin_fmaf(d, L2E_LO, __builtin_fmaf(d, L2E_HI, -h));
-    const bool tiny = h < -120.0f;
-    const float z = __builtin_amdgcn_exp2f(tiny ? h - (float)ue : h);
-    const float tz = __builtin_fmaf(z, l * LN2_F, z);
-    const float t = tiny ? tz : __builtin_ldexpf(tz, -ue);
-    const float rho = tiny ? __builtin_fmaf(fabsf(h) + 160.0f, 0x1p-24f, RHO0) : RHO0;
-    const float qf = __builtin_rintf(t);
-    sure = dok & (__builtin_fmaf(t, rho, fabsf(t - qf)) < 0.5f) & (t < 8388608.0f);
-    return (uint32_t)qf;
-}
-
-// The term's lower bound for the running-sum prediction: exactly 1 for the row maximum's
-// value (exp(0)), else the cheap estimate less its error.
-__device__ __forceinline__ float term_lb(float x, float ev, float xmax, float M) {
-    return x == xmax ? 1.0f : ev * (1.0f - 0x1p-12f - fabsf(M) * 0x1p-22f);
+// The terms e = expf(fl(x / T) - M) of a thread's elements, exactly as the reference
+// computes them (sample.rs:373-385). MODE 0: T = 1 (x / T = x); 1: Markstein's corrected
+// quotient (exact for |x| in [2^-100, 2^100) and T in [2^-20, 2^20]; outside that range of
+// x, |x / T| lies below 2^-80, where fl(s - M) = -M for the |M| >= 2^-50 the mode requires,
+// or above 2^80 > |M|, where it is negative enough that e is 0, or -inf / NaN for a masked
+// element, whose e is 0); 2: IEEE division.
+template <int MODE, int QV, int EPV>
+__device__ __forceinline__ void exact_terms(const float (&x)[QV][EPV], float (&ev)[QV][EPV], float T, float rT,
+                                            float M, const uint64_t* tab) {
+#pragma unroll
+    for (int q = 0; q < QV; q++)
+#pragma unroll
+        for (int e = 0; e < EPV; e++) {
+            float s;
+            if (MODE == 0) {
+                s = x[q][e];
+            } else if (MODE == 1) {
+                const float q0 = x[q][e] * rT;
+                const float r0 = __builtin_fmaf(-q0, T, x[q][e]);
+                s = __builtin_fmaf(r0, rT, q0);
+            } else {
+                s = x[q][e] / T;
+            }
+            ev[q][e] = expf_nonpos(s - M, tab);
+            if (e == EPV - 1) __builtin_amdgcn_sched_barrier(0);  // a vector at a time: bounded registers
+        }
 }
 
 template <bool BF16, int QV, bool FULL>
@@ -129,7 +126,8 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                                             uint32_t c1) {
     constexpr int EPV = Elem<BF16>::EPV;
     static_assert(QV <= QVMAX, "per-vector tables");
-    const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+    const int tid = threadIdx.x, lane = lane_id();
+    const int w = __builtin_amdgcn_readfirstlane(wave_id());
     const uint32_t em = (1u << EPV) - 1u;
     const int nc = a.n_chunks;
     const int64_t rc = (int64_t)row * nc + chunk;
@@ -148,21 +146,23 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
     float x[QV][EPV];
     if (FULL) load_full_tile<BF16, QV>(a, row, c0, x);
     else load_tile<BF16, QV>(a, row, c0, c1, x);
+    if (tid < 32) sm.etab[tid] = EXP2_32[tid];
     const RowCtx C = make_ctx(a, row);
     if (!C.active) return;
     const float M = ld_uniform(&a.rinfo[row].M);
     if (!quant_row(C, M)) return;
     const float th = ld_uniform(&a.rinfo[row].th);
-    const float xmax = ld_uniform(&a.rinfo[row].xmax);
     const float xm = ld_uniform(&a.parts[rc].xm);
     const float Pc = ld_uniform(&a.qpre[rc].P);
     const float Lc = ld_uniform(&a.qpre[rc].lb);
     QHead* const head = a.qhead + rc;
     QItem* const items = a.qitem + rc * (a.qcap + 1);
     const float Kc = -(M * 1.44269504088896341f);
-    // candidates: (x / T - M) log2(e) estimated as x * rTl + Kc, above the bound less the
-    // estimate's error (the roundings of x / T, of M and of the products, in log2-units)
+    // candidates: the row's bound th on (x / T - M) log2(e), less the margin its estimates
+    // carry (the roundings of x / T, of M and of the products, in log2-units); an element is
+    // a candidate when its exact term reaches 2^gth, lowered once more for exp2's rounding
     const float gth = th - (0x1p-8f + (fabsf(M) * 12.0f + 200.0f) * 0x1p-24f);
+    const float egth = gth > -__builtin_inff() ? __builtin_amdgcn_exp2f(gth) * (1.0f - 0x1p-10f) : 0.0f;
     const float amax = xm > -__builtin_inff() ? __builtin_fmaf(xm, C.rTl, Kc) : -__builtin_inff();
     const bool gather = amax >= gth;
     // a chunk whose largest term is below half a unit of the predicted running sum's lowest
@@ -198,8 +198,8 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             const uint32_t d = hid[g] - c0;
             if (hid[g] < c1 && hid[g] >= c0) lds_add(&sm.hc[d >> 1], 1u << (16 * (d & 1u)));
         }
-        __syncthreads();
     }
+    __syncthreads();  // (the history counts and the expf table)
 #pragma unroll
     for (int q = 0; q < QV; q++) {
         const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
@@ -236,69 +236,66 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
     }
     BFI_TRACE(a, tb, 2);
 
+    // the exact terms, and the candidates among them
+    float ev[QV][EPV];
+    {
+        const float aM = fabsf(M);
+        if (C.T == 1.0f) exact_terms<0, QV, EPV>(x, ev, C.T, C.rT, M, sm.etab);
+        else if (C.fast_div && aM >= 0x1p-50f && aM < 0x1p80f) exact_terms<1, QV, EPV>(x, ev, C.T, C.rT, M, sm.etab);
+        else exact_terms<2, QV, EPV>(x, ev, C.T, C.rT, M, sm.etab);
+    }
+    uint32_t tk[QV];
+#pragma unroll
+    for (int q = 0; q < QV; q++) {
+        tk[q] = 0;
+#pragma unroll
+        for (int e = 0; e < EPV; e++) tk[q] |= (ev[q][e] >= egth && x[q][e] > -__builtin_inff()) ? 1u << e : 0u;
+    }
+
     uint32_t qflags = QF_EXACT, qn = 0;  // this chunk's summary (for the first chunk's walk below)
     if (!trivial) {
-        // the prediction: cheap estimates e ~ 2^(x rTl + Kc) (shifted below 2^-120), their
-        // prefix sums and the largest term's lower bound so far (index order: vector,
-        // thread, element), from the row's values at the chunk's start
-        float ev[QV][EPV];
-        float vpre[QV], vmx[QV], vsum[QV], vtop[QV];
+        // the prediction: prefix sums of the terms (index order: vector, thread, element) from
+        // the row's values at the chunk's start, and a lower bound: 1 once a term equal to 1
+        // (the row maximum's, exp(0)) has been added (the element walk below also raises it
+        // to each term it passes)
+        float vpre[QV], vmx[QV], vsum[QV];
 #pragma unroll
         for (int q = 0; q < QV; q++) {
-            float g = 0.0f, gm = 0.0f, gt = 0.0f;
+            float g = 0.0f;
+            bool one = false;
 #pragma unroll
             for (int e = 0; e < EPV; e++) {
-                const float a_ = __builtin_fmaf(x[q][e], C.rTl, Kc);
-                const float z = __builtin_amdgcn_exp2f(a_ < -120.0f ? a_ + 64.0f : a_);
-                ev[q][e] = x[q][e] > -__builtin_inff() ? (a_ < -120.0f ? __builtin_ldexpf(z, -64) : z) : 0.0f;
                 g += ev[q][e];
-                gt = fmaxf(gt, ev[q][e]);
-                gm = fmaxf(gm, term_lb(x[q][e], ev[q][e], xmax, M));
+                one = one || ev[q][e] == 1.0f;
             }
             vsum[q] = g;
-            vtop[q] = gt;
             const float incl = wave_scan_incl(g, 0.0f, [](float u, float v) { return u + v; });
-            const float inclm = wave_scan_incl(gm, 0.0f, [](float u, float v) { return fmaxf(u, v); });
+            const uint64_t ob = __ballot(one);
             if (lane == WAVE - 1) {
-                sm.vs[q][w] = incl;
-                sm.vm[q][w] = inclm;
+                sm.vs[q * NWAVE + w] = incl;
+                sm.vm[q * NWAVE + w] = ob ? 1.0f : 0.0f;
             }
             vpre[q] = wave_excl_of_incl(incl, 0.0f);
-            vmx[q] = wave_excl_of_incl(inclm, 0.0f);
+            vmx[q] = (ob & lanes_below()) ? 1.0f : 0.0f;
         }
         __syncthreads();
         {
-            float run = Pc, runm = Lc;
+            float spre[QV], smax[QV];
+            slot_prefix<QV>(sm.vs, sm.vm, w, spre, smax);
 #pragma unroll
             for (int q = 0; q < QV; q++) {
-                float tot = 0.0f, mine = 0.0f, totm = 0.0f, minem = 0.0f;
-#pragma unroll
-                for (int ww = 0; ww < NWAVE; ww++) {
-                    const float v = sm.vs[q][ww], vm = sm.vm[q][ww];
-                    mine += ww < w ? v : 0.0f;
-                    minem = ww < w ? fmaxf(minem, vm) : minem;
-                    tot += v;
-                    totm = fmaxf(totm, vm);
-                }
-                vpre[q] += run + mine;
-                vmx[q] = fmaxf(vmx[q], fmaxf(runm, minem));
-                run += tot;
-                runm = fmaxf(runm, totm);
+                vpre[q] += Pc + spre[q];
+                vmx[q] = fmaxf(vmx[q], fmaxf(Lc, smax[q]));
             }
         }
         BFI_TRACE(a, tb, 3);
-        // classify and quantize: window bits (the interval straddles a binade boundary, or
-        // the estimate lies near a rounding boundary: the chain adds these exactly) and zero
-        // bits (masked: they add nothing at any binade). The running sums below 2^-125 (the
-        // subnormals and the lowest normal binade) share one spacing, 2^-149: one binade.
-        // The units come from the precise estimate: s = fl(x / T) exactly (Markstein's
-        // corrected quotient), d = fl(s - M) as the reference rounds it, exp(d) = 2^(h + l)
-        // with h = fl(d log2(e)) and l its rounding error plus log2(e)'s own, as
-        // exp2(h) (1 + l ln 2), within RHO0 of glibc's expf(d). A certain element keeps
-        // (units << 8 | ue + 150) (its units are below 2^23).
+        // classify and quantize: window bits (the interval straddles a binade boundary, a tie
+        // of RN, or 2^23 units or more: the chain adds these exactly) and zero bits (e = 0:
+        // nothing at any binade). The running sums below 2^-125 (the subnormals and the
+        // lowest normal binade) share one spacing, 2^-149: one binade. A certain element
+        // keeps (units << 8 | ue + 150).
         uint32_t pk[QV][EPV];
-        uint32_t wm[QV], zm[QV], vs1[QV];  // vs1: the vector lies in one binade (its elo), else 0
-        const bool fdiv = __builtin_amdgcn_readfirstlane(C.fast_div ? 1 : 0) != 0;
+        uint32_t wm[QV], zm[QV];
 #pragma unroll
         for (int q = 0; q < QV; q++) {
             // the vector as a whole: the interval from before its first element to after its
@@ -306,10 +303,8 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             const float vlo = fmaxf(vpre[q] * (1.0f - QEPS), vmx[q]);
             const float vhi = (vpre[q] + vsum[q]) * (1.0f + QEPS);
             const uint32_t velo = max(__float_as_uint(vlo) >> 23, 1u), vehi = max(__float_as_uint(vhi) >> 23, 1u);
-            const bool same = velo == vehi;
-            vs1[q] = same ? velo : 0u;
             uint32_t elo_e[EPV], wq = 0, zq = 0;
-            if (same) {
+            if (velo == vehi) {
 #pragma unroll
                 for (int e = 0; e < EPV; e++) elo_e[e] = velo;
             } else {
@@ -324,30 +319,20 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                     elo_e[e] = elo;
                     wq |= elo != ehi ? 1u << e : 0u;
                     A = An;
-                    L = fmaxf(L, term_lb(x[q][e], v, xmax, M));
+                    L = fmaxf(L, v);
                 }
             }
-            // the units; a vector whose largest term is below a quarter unit adds nothing
-            const bool negl = same & (__builtin_ldexpf(vtop[q], -((int32_t)velo - 150)) < 0.25f) &
-                              (vtop[q] >= 0x1p-120f);
 #pragma unroll
             for (int e = 0; e < EPV; e++) {
-                const bool zero = !(x[q][e] > -__builtin_inff());
+                const bool zero = !(ev[q][e] > 0.0f);
+                const float t = __builtin_ldexpf(ev[q][e], 150 - (int32_t)elo_e[e]);
+                const float qf = __builtin_rintf(t);
+                const bool win = !zero & (((wq >> e) & 1u) | (fabsf(t - qf) == 0.5f) | !(t < 8388608.0f));
                 zq |= zero ? 1u << e : 0u;
-                pk[q][e] = zero ? 0u : (elo_e[e] & 0xFFu);  // (no units: checked at this binade)
+                wq = win ? wq | (1u << e) : wq & ~(1u << e);
+                pk[q][e] = (zero | win) ? 0u : ((uint32_t)qf << 8) | (elo_e[e] & 0xFFu);
             }
-            if (!negl) {
-#pragma unroll
-                for (int e = 0; e < EPV; e++) {
-                    bool sure;
-                    const uint32_t u = elem_units(x[q][e], elo_e[e], fdiv, C.T, C.rT, M, sure);
-                    const bool zero = (zq >> e) & 1u;
-                    const bool win = !zero & (((wq >> e) & 1u) | !sure);
-                    wq = win ? wq | (1u << e) : wq & ~(1u << e);
-                    pk[q][e] = (zero | win) ? 0u : (u << 8) | (elo_e[e] & 0xFFu);
-                }
-            }
-            wm[q] = wq & ~zq;
+            wm[q] = wq;
             zm[q] = zq;
         }
         BFI_TRACE(a, tb, 4);
@@ -357,32 +342,23 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         for (int q = 0; q < QV; q++) {
             const uint32_t c = (uint32_t)__popc(wm[q]);
             const uint32_t incl = wave_scan_incl(c, 0u, [](uint32_t u, uint32_t v) { return u + v; });
-            if (lane == WAVE - 1) sm.vc[q][w] = incl;
+            if (lane == WAVE - 1) sm.vc[q * NWAVE + w] = incl;
             wpre[q] = incl - c;
         }
         __syncthreads();
         uint32_t nwin;
         {
-            uint32_t run = 0;
+            const uint32_t tv = lane < QV * NWAVE ? sm.vc[lane] : 0u;
+            const uint32_t ti = wave_scan_incl(tv, 0u, [](uint32_t u, uint32_t v) { return u + v; });
+            const uint32_t te = ti - tv;
+            nwin = (uint32_t)__builtin_amdgcn_readlane((int)ti, QV * NWAVE - 1);
 #pragma unroll
-            for (int q = 0; q < QV; q++) {
-                uint32_t tot = 0, mine = 0;
-#pragma unroll
-                for (int ww = 0; ww < NWAVE; ww++) {
-                    const uint32_t v = sm.vc[q][ww];
-                    mine += ww < w ? v : 0u;
-                    tot += v;
-                }
-                wpre[q] += run + mine;
-                run += tot;
-            }
-            nwin = run;
+            for (int q = 0; q < QV; q++) wpre[q] += (uint32_t)__builtin_amdgcn_readlane((int)te, q * NWAVE + w);
         }
         uint32_t flags = nwin > (uint32_t)a.qcap ? QF_EXACT : 0u;
         uint32_t bad = 0;
         if (!flags) {
-            // the windows' (index, x) into their items (the exact values come below), the run
-            // tables cleared
+            // the windows' (index, e) into their items, the run tables cleared
 #pragma unroll
             for (int q = 0; q < QV; q++) {
                 const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
@@ -391,10 +367,10 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                 while (m) {
                     const int i = __builtin_ctz(m);
                     m &= m - 1u;
-                    float xe = x[q][0];
+                    float ee = ev[q][0];
 #pragma unroll
-                    for (int e = 1; e < EPV; e++) xe = e == i ? x[q][e] : xe;
-                    *reinterpret_cast<uint2*>(&items[pos]) = make_uint2(id0 + (uint32_t)i, __float_as_uint(xe));
+                    for (int e = 1; e < EPV; e++) ee = e == i ? ev[q][e] : ee;
+                    *reinterpret_cast<uint2*>(&items[pos]) = make_uint2(id0 + (uint32_t)i, __float_as_uint(ee));
                     pos++;
                 }
             }
@@ -496,7 +472,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                 if (k < nwin) {
                     const uint2 wv = *reinterpret_cast<const uint2*>(&items[k]);
                     it.id = wv.x;
-                    it.e = quant_exact(__uint_as_float(wv.y), C.T, C.rT, C.fast_div ? 1 : 0, M);
+                    it.e = __uint_as_float(wv.y);
                 }
                 it.q = q;
                 it.ue = ue;
@@ -517,19 +493,12 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         if (a.trace && tid == 0) a.trace[tb + 6] = nwin;  // diagnostics: windows
     }
 
-    // the candidates of the kept set into the row's list: positions from a block scan, one
-    // global count per workgroup
+    // the candidates of the kept set into the row's list, as (id, e): positions from a block
+    // scan, one global count per workgroup
     if (gather) {
-        uint32_t tk[QV];
         uint32_t nt = 0;
 #pragma unroll
-        for (int q = 0; q < QV; q++) {
-            tk[q] = 0;
-#pragma unroll
-            for (int e = 0; e < EPV; e++)
-                tk[q] |= (x[q][e] > -__builtin_inff() && __builtin_fmaf(x[q][e], C.rTl, Kc) >= gth) ? 1u << e : 0u;
-            nt += (uint32_t)__popc(tk[q]);
-        }
+        for (int q = 0; q < QV; q++) nt += (uint32_t)__popc(tk[q]);
         uint32_t tot;
         uint32_t pos = block_excl_scan<uint32_t>(nt, sm.wg, tot);
         if (tot) {
@@ -544,10 +513,10 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                 while (m) {
                     const int i = __builtin_ctz(m);
                     m &= m - 1u;
-                    float xe = x[q][0];
+                    float ee = ev[q][0];
 #pragma unroll
-                    for (int e = 1; e < EPV; e++) xe = e == i ? x[q][e] : xe;
-                    if (pos < (uint32_t)a.V) list[pos] = ((uint64_t)(id0 + (uint32_t)i) << 32) | __float_as_uint(xe);
+                    for (int e = 1; e < EPV; e++) ee = e == i ? ev[q][e] : ee;
+                    if (pos < (uint32_t)a.V) list[pos] = ((uint64_t)(id0 + (uint32_t)i) << 32) | __float_as_uint(ee);
                     pos++;
                 }
             }

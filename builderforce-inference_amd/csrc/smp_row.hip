@@ -526,7 +526,9 @@ __device__ __forceinline__ void row_decode(const StreamArgs& A, const RawT<BF16,
     }
 }
 
-// Appends (id, x) to the row's candidate list (the first V entries of its spill area).
+// Appends (id, e) to the row's candidate list (the first V entries of its spill area): e is
+// the element's exact term expf(fl(x / T) - M) (sample.rs:374, 383), computed here for the
+// few elements taken.
 __device__ __forceinline__ void list_append(const StreamArgs& A, bool take, uint32_t id, float x) {
     const uint64_t bal = __ballot(take);
     if (!bal) return;
@@ -536,7 +538,8 @@ __device__ __forceinline__ void list_append(const StreamArgs& A, bool take, uint
     base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
     if (take) {
         const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
-        if (pos < A.V) gl(A.spill)[pos] = ((uint64_t)id << 32) | __float_as_uint(x);
+        const float e = exact_value(x, A.T, A.rT, A.fast_div, A.M, 1.0f, 0);
+        if (pos < A.V) gl(A.spill)[pos] = ((uint64_t)id << 32) | __float_as_uint(e);
     }
 }
 
@@ -749,7 +752,8 @@ struct ListInfo {
     uint32_t nb;        // buckets in use
     uint64_t kmax;      // the largest key
     int row;
-    int small;          // n <= SORTCAP: the keys sorted in LDS (G = the LDS list), no buckets
+    int small;          // n <= SORTCAP: the keys sorted in LDS, no buckets
+    float* cum;         // small lists: LDS room for a walk's running sum after each element
 };
 
 __device__ __forceinline__ float key_p(uint64_t key, bool idxmode) {
@@ -763,9 +767,9 @@ __device__ __forceinline__ uint64_t make_key(float p, uint32_t id, bool idxmode)
                    : (((uint64_t)(0x80000000u | __float_as_uint(p)) << 32) | (uint64_t)(~id));
 }
 
-// Turns the N gathered (id, x) entries of the row's list into keys, keeps those with
-// p >= p_lo (> 0), compacted (LDS, then the row's spill area from 2V), and groups them by
-// bucket; at most WAVE keys are sorted by one wave instead. Every thread calls it.
+// Turns the N gathered (id, e) entries of the row's list (e: the exact term) into keys, keeps
+// those with p >= p_lo (> 0), compacted (LDS, then the row's spill area from 2V), and groups
+// them by bucket; at most WAVE keys are sorted by one wave instead. Every thread calls it.
 __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t N, float M,
                                                float S, float p_lo, bool idxmode) {
     const int tid = threadIdx.x;
@@ -779,8 +783,7 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
     for (uint32_t j = tid; j < N; j += BLOCK) {
         const uint64_t ent = src[j];
         const uint32_t id = (uint32_t)(ent >> 32);
-        const float xv = __uint_as_float((uint32_t)ent);
-        const float p = xv > -__builtin_inff() ? exact_value(xv, C.T, C.rT, C.fast_div, M, S, 1) : 0.0f;
+        const float p = exact_p(__uint_as_float((uint32_t)ent), S);
         const bool valid = p > 0.0f && p >= p_lo;
         const uint64_t key = make_key(p, id, idxmode);
         const uint64_t bal = __ballot(valid);
@@ -810,6 +813,7 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
         // small: one wave sorts the keys into LDS
         L.small = 1;
         L.G = sm.list;
+        L.cum = reinterpret_cast<float*>(sm.grp);
         if (wave_id() == 0) {
             const int lane = lane_id();
             uint64_t key = (uint32_t)lane < nv ? sm.list[lane] : 0ull;
@@ -823,34 +827,36 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
         return L;
     }
     if (nv <= (uint32_t)SORTCAP) {
-        // medium: a block-wide bitonic sort (descending) of the keys, zero-padded to a power
-        // of two, in LDS
+        // medium: each key goes to its rank, the count of larger keys (keys are distinct:
+        // their ids differ); every thread ranks up to two keys in one pass over the list
+        static_assert(SORTCAP <= 2 * BLOCK, "two keys per thread");
         L.small = 1;
-        L.G = sm.list;
-        uint32_t n2 = WAVE;
-        while (n2 < nv) n2 <<= 1;
-        for (uint32_t j = nv + (uint32_t)tid; j < n2; j += BLOCK) sm.list[j] = 0ull;
-        __syncthreads();
-        for (uint32_t size = 2; size <= n2; size <<= 1) {
-            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-                for (uint32_t i = (uint32_t)tid; i < n2 / 2; i += BLOCK) {
-                    const uint32_t lo = 2 * i - (i & (stride - 1));
-                    const uint32_t hi = lo + stride;
-                    const bool desc = (lo & size) == 0;
-                    const uint64_t x = sm.list[lo], y = sm.list[hi];
-                    if ((x < y) == desc) {
-                        sm.list[lo] = y;
-                        sm.list[hi] = x;
-                    }
-                }
-                __syncthreads();
+        uint64_t* out = sm.grp;
+        const uint32_t i0 = (uint32_t)tid, i1 = (uint32_t)tid + BLOCK;
+        const uint64_t k0 = i0 < nv ? sm.list[i0] : ~0ull;  // (~0: no key, outranks nothing)
+        const uint64_t k1 = i1 < nv ? sm.list[i1] : ~0ull;
+        uint32_t r0 = 0, r1 = 0;
+        if (nv > (uint32_t)BLOCK) {
+#pragma unroll 4
+            for (uint32_t j = 0; j < nv; j++) {
+                const uint64_t kj = sm.list[j];
+                r0 += kj > k0 ? 1u : 0u;
+                r1 += kj > k1 ? 1u : 0u;
             }
+        } else {
+#pragma unroll 8
+            for (uint32_t j = 0; j < nv; j++) r0 += sm.list[j] > k0 ? 1u : 0u;
         }
-        L.kmax = sm.list[0];
+        if (i0 < nv) out[r0] = k0;
+        if (i1 < nv) out[r1] = k1;
         __syncthreads();
+        L.G = out;
+        L.cum = reinterpret_cast<float*>(sm.list);
+        L.kmax = out[0];
         return L;
     }
     L.small = 0;
+    L.cum = nullptr;
     // reductions: max/min of the high words, the largest key
     {
         const uint32_t wmx = lane63(wave_scan_incl(hmax, 0u, [](uint32_t x, uint32_t y) { return max(x, y); }));
@@ -1012,7 +1018,7 @@ __device__ __forceinline__ void walk_set(WalkState& w, float s, float th) {
 // Element-level walk over one wave-load of sorted keys (one per lane, 0 = none). Returns
 // true when it stopped (o filled). Wave-uniform.
 __device__ __forceinline__ bool walk_elems(WalkState& w, uint64_t key, float th, uint32_t R, uint64_t excl,
-                                           bool idxmode, WalkOut& o) {
+                                           bool idxmode, WalkOut& o, float* cum) {
     const int lane = lane_id();
     int done = -1;
     for (;;) {
@@ -1027,12 +1033,14 @@ __device__ __forceinline__ bool walk_elems(WalkState& w, uint64_t key, float th,
         const uint32_t run = sat_add(w.m, Qi);
         const bool ev = valid && (tie || run >= M_TOP || run >= w.tu || (uint64_t)w.r + Ci >= (uint64_t)R);
         const uint64_t bal = __ballot(ev);
+        const int j = bal ? __ffsll((unsigned long long)bal) - 1 : WAVE;
+        // the elements before the first event are settled: their running sums
+        if (cum && valid && lane < j) cum[w.r + Ci - 1] = state_value(run, w.ue);
         if (!bal) {
             w.m = lane63(run);
             w.r += lane63(Ci);
             return false;
         }
-        const int j = __ffsll((unsigned long long)bal) - 1;
         const uint32_t run_j = (uint32_t)__builtin_amdgcn_readlane((int)run, j);
         const uint32_t runb = j ? (uint32_t)__builtin_amdgcn_readlane((int)run, j - 1) : w.m;
         const uint32_t ci_j = (uint32_t)__builtin_amdgcn_readlane((int)Ci, j);
@@ -1045,9 +1053,11 @@ __device__ __forceinline__ bool walk_elems(WalkState& w, uint64_t key, float th,
             o.rank = rank_j;
             o.key = key_j;
             o.how = run_j >= w.tu ? 1 : 2;
+            if (cum && lane == 0) cum[rank_j] = o.cum;
             return true;
         }
         const float sn = state_value(runb, w.ue) + key_p(key_j, idxmode);
+        if (cum && lane == 0) cum[rank_j] = sn;
         if (sn >= th || (uint64_t)w.r + ci_j >= (uint64_t)R) {
             o.cum = sn;
             o.rank = rank_j;
@@ -1063,7 +1073,7 @@ __device__ __forceinline__ bool walk_elems(WalkState& w, uint64_t key, float th,
 
 // The walk, done by wave 0 (the result is broadcast through LDS to every thread).
 __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
-                                     uint64_t* gscratch) {
+                                     uint64_t* gscratch, float* cum = nullptr) {
     RowSmem& sm = g_sm;
     WalkOut o{0.0f, 0u, 0ull, 0};
     if (wave_id() == 0) {
@@ -1073,7 +1083,7 @@ __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, 
         w.r = 0;
         bool stopped = false;
         for (uint32_t j0 = 0; L.small && j0 < L.n && !stopped; j0 += WAVE)
-            stopped = walk_elems(w, j0 + (uint32_t)lane < L.n ? sm.list[j0 + lane] : 0ull, th, R, excl, idxmode, o);
+            stopped = walk_elems(w, j0 + (uint32_t)lane < L.n ? L.G[j0 + lane] : 0ull, th, R, excl, idxmode, o, cum);
         uint32_t b0 = 0;
         while (!L.small && b0 < L.nb && !stopped) {
             const uint32_t b = b0 + (uint32_t)lane;
@@ -1111,13 +1121,13 @@ __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, 
             if (n <= (uint32_t)WAVE) {
                 uint64_t key = (uint32_t)lane < n ? L.G[o0 + lane] : 0ull;
                 key = wave_sort_desc(key);
-                stopped = walk_elems(w, key, th, R, excl, idxmode, o);
+                stopped = walk_elems(w, key, th, R, excl, idxmode, o, nullptr);
             } else {
                 int n2 = WAVE;
                 while ((uint32_t)n2 < n) n2 <<= 1;
                 const uint64_t* buf = sort_bucket(gscratch, L.G + o0, n, n2);
                 for (int j0 = 0; j0 < (int)n && !stopped; j0 += WAVE)
-                    stopped = walk_elems(w, buf[j0 + lane], th, R, excl, idxmode, o);
+                    stopped = walk_elems(w, buf[j0 + lane], th, R, excl, idxmode, o, nullptr);
             }
             b0 = bs + 1;
         }
@@ -1151,7 +1161,7 @@ __device__ __forceinline__ void list_kept(const ListInfo L, uint32_t* ids, float
     RowSmem& sm = g_sm;
     if (L.small) {
         for (uint32_t j = (uint32_t)threadIdx.x; j < lim; j += BLOCK) {
-            const uint64_t key = sm.list[j];
+            const uint64_t key = L.G[j];
             ids[j] = key_id(key, idxmode);
             probs[j] = key_p(key, idxmode);
         }
@@ -1493,6 +1503,29 @@ __device__ __forceinline__ StreamArgs stream_args(const KArgs& a, const RowCtx& 
     return A;
 }
 
+// The first index i < n with cum[i] >= r (n when none); cum is non-decreasing (a running sum
+// of non-negative terms). Wave 0 searches in two rounds of 64 probes; every thread gets it.
+__device__ __forceinline__ uint32_t first_ge(const float* cum, uint32_t n, float r, RowSmem& sm) {
+    if (wave_id() == 0) {
+        const uint32_t lane = (uint32_t)lane_id();
+        const uint32_t seg = (n + WAVE - 1) / WAVE;  // segment length (n <= 64 * 64)
+        const uint32_t e = min((lane + 1) * seg, n);  // this lane's segment end
+        const uint64_t hit = __ballot(e > lane * seg && cum[e - 1] >= r);
+        uint32_t res = n;
+        if (hit) {
+            const uint32_t s0 = (uint32_t)(__ffsll((unsigned long long)hit) - 1) * seg;
+            const uint32_t j = s0 + lane;
+            const uint64_t h2 = __ballot(lane < seg && j < n && cum[j] >= r);
+            res = s0 + (uint32_t)(__ffsll((unsigned long long)h2) - 1);
+        }
+        if (lane == 0) sm.misc[MS_STOP] = res;
+    }
+    __syncthreads();
+    const uint32_t res = sm.misc[MS_STOP];
+    __syncthreads();
+    return res;
+}
+
 template <bool BF16>
 __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
     const int tid = threadIdx.x;
@@ -1607,11 +1640,15 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
             const float p_lo = exhaustive ? 0.0f : (float)(exp2((double)th) / (double)S * (1.0 + 0x1p-20));
             const ListInfo L = build_list(a, sm, C, N, M, S, p_lo, false);
             BFI_RTRACE(a, C, 5);
-            // top-p (sample.rs:397-409)
+            // top-p (sample.rs:397-409); a sampled row's walks over a small list keep the
+            // running sum after each element, from which the kept sum and the draw are read
+            float* const cum = C.judged ? nullptr : L.cum;
+            uint32_t ncum = 0;  // elements with a kept running sum
             uint32_t Lp = Lk;
             WalkOut o1{0.0f, 0u, 0ull, 0};
             if (C.pmode) {
-                o1 = walk(L, C.top_p, Lk, 0ull, 0, gscr);
+                o1 = walk(L, C.top_p, Lk, 0ull, 0, gscr, cum);
+                if (cum) ncum = o1.how ? o1.rank + 1 : o1.rank;
                 if (o1.how == 1) Lp = o1.rank + 1;
                 else if (o1.how == 0 && !exhaustive) Lp = LINF;
             }
@@ -1656,17 +1693,30 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
             if (C.pmode && o1.how == 1 && Lfin == Lp) {
                 sum = o1.cum;
                 klast = o1.key;
+            } else if (cum && npos == Lfin && Lfin <= ncum) {
+                sum = cum[Lfin - 1];  // (not a judged row: klast unused)
+                klast = 0ull;
             } else {
-                const WalkOut o2 = walk(L, __builtin_inff(), Lfin, 0ull, 0, gscr);
+                const WalkOut o2 = walk(L, __builtin_inff(), Lfin, 0ull, 0, gscr, cum);
                 sum = o2.cum;
                 klast = o2.how == 2 ? o2.key : 0ull;
+                if (cum) ncum = o2.how ? o2.rank + 1 : o2.rank;
             }
             put_stats(a, C, M, S, sum, 1.0f);
             BFI_RTRACE(a, C, 7);
             if (!C.judged) {  // draw (sample.rs:312-323)
                 const float r = C.u * fmaxf(sum, 0.0f);
-                const WalkOut o3 = walk(L, r, Lfin, 0ull, 0, gscr);
-                const uint32_t tok = o3.how ? key_id(o3.key, false) : 0u;
+                uint32_t tok;
+                if (cum && min(Lfin, L.n) <= ncum) {
+                    // the first kept element whose running sum reaches r, else the Lfin-th
+                    // (the walk's stop at R), else none
+                    const uint32_t nk = min(Lfin, L.n);
+                    const uint32_t i = first_ge(cum, nk, r, sm);
+                    tok = i < nk ? key_id(L.G[i], false) : (Lfin <= L.n ? key_id(L.G[Lfin - 1], false) : 0u);
+                } else {
+                    const WalkOut o3 = walk(L, r, Lfin, 0ull, 0, gscr);
+                    tok = o3.how ? key_id(o3.key, false) : 0u;
+                }
                 BFI_RTRACE(a, C, 8);
                 if (a.t_kind) {
                     const uint32_t lim = (uint32_t)min((int64_t)npos, a.t_cap);

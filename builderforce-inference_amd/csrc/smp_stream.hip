@@ -163,7 +163,7 @@ __device__ __forceinline__ void finish_row(const KArgs& a, StreamSmem& sm, int r
         R.S_apx = (float)tot;
         const bool list_mode = C.kmode || C.pmode || C.mmode;
         float th = -__builtin_inff();
-        if ((C.kmode || C.pmode) && !C.pen_hash && R.xmax > -__builtin_inff())
+        if ((C.kmode || C.pmode) && !(C.min_p >= 0x1p-10f) && !C.pen_hash && R.xmax > -__builtin_inff())
             th = gather_bound(a, sm, C, R.xmax, tot * (1.0 + 1e-4));
         if (C.mmode) th = fmaxf(th, log2f(C.min_p) - 0x1p-6f);
         if (list_mode) R.th = th;
@@ -346,7 +346,10 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
     }
     // the histogram's bins, cleared while the exchange above settles (the history counts
     // in the same words are all read by now)
-    const bool want_hist = !C.greedy && (C.kmode || C.pmode) && a.vhist != nullptr;
+    // (rows with min_p >= 2^-10 skip it: every kept element has p >= min_p * max p,
+    // sample.rs:411-414, so the min-p bound alone keeps the candidates within 10 log2-units
+    // of the maximum)
+    const bool want_hist = !C.greedy && (C.kmode || C.pmode) && !(C.min_p >= 0x1p-10f) && a.vhist != nullptr;
     if (want_hist) {
         if (C.prepen) __syncthreads();
         for (int i = tid; i < HBINS; i += BLOCK) sm.hc[i] = 0u;
