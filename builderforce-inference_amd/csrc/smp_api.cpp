@@ -155,7 +155,7 @@ Layout layout(int64_t n_rows, int64_t V, const Shape& s, int bm_words) {
     L.parts = off;
     off = align_up(off + (size_t)n_rows * s.n_chunks * sizeof(bfi::ChunkPart), 256);
     L.vhist = off;
-    off = align_up(off + (size_t)n_rows * s.n_chunks * bfi::HBINS * sizeof(uint32_t), 256);
+    off = align_up(off + (size_t)n_rows * s.n_chunks * 2 * bfi::HBINS * sizeof(uint32_t), 256);
     L.row_res = off;
     off = align_up(off + (size_t)n_rows * 2 * sizeof(uint32_t), 256);
     L.row_pen = off;

@@ -25,7 +25,7 @@ constexpr int NCMAX = 256;             // chunks per row
 constexpr int PREPEN_H = 1024;         // histories up to this length are applied by the stream pass
 constexpr int GDCAP = 4096;            // distinct history ids counted per row (global tables)
 constexpr int HBINS = 128;             // bins of the stream pass's per-chunk value histogram
-constexpr int HBIN_PER_LOG2 = 8;       // bins per log2-unit below the chunk maximum
+constexpr int HBIN_PER_LOG2 = 4;       // bins per log2-unit below the chunk maximum (32 units)
 constexpr float F32_EPS = 1.1920928955078125e-07f;  // f32::EPSILON
 
 // Per (row, chunk) result of the streaming pass over the values s = x / T of the masked
@@ -116,7 +116,7 @@ struct KArgs {
     uint32_t* out_next;
     // workspace
     ChunkPart* parts;
-    uint32_t* vhist;     // per (row, chunk): HBINS counts (top-k / top-p rows)
+    uint32_t* vhist;     // per (row, chunk): HBINS 64-bit bins, count | fixed-point mass (top-k / top-p rows)
     uint32_t* seq_ctr;
     uint32_t* row_res;   // verify: 2 words per row {verdict, token}
     uint32_t* row_pen;   // per row: history bitmap[bm_words] + popcount prefix[bm_words] + counts[GDCAP]

@@ -1071,9 +1071,206 @@ __device__ __forceinline__ bool walk_elems(WalkState& w, uint64_t key, float th,
     }
 }
 
-// The walk, done by wave 0 (the result is broadcast through LDS to every thread).
+// ---- walks over a bucketed (large) list ----------------------------------------------
+//
+// Rounds over the keys in bucket order, the whole block at once: from the walk's state,
+// each thread takes WPT consecutive keys of a tile of whole buckets, their unit counts at
+// the state's binade and their ranks come from a block scan, and the first key at which
+// an event occurs (the sum leaving its binade, reaching the threshold, a tie of RN, the
+// R-th element) names the bucket to walk element by element: the buckets before it are
+// added whole (inside a bucket the order does not change a sum that stays in one binade
+// without ties), that bucket is sorted and walked by one wave, and the next round starts
+// after it.
+
+constexpr int WPT = 16;                           // keys per thread per round
+constexpr uint32_t WTILE = (uint32_t)BLOCK * WPT;  // keys per round
+
+// The first key of bucket b (b == nb: the list's end).
+__device__ __forceinline__ uint32_t bucket_start(const RowSmem& sm, const ListInfo& L, uint32_t b) {
+    return b < L.nb ? sm.boff[b] : L.n;
+}
+// Largest bucket b in [lo, hi) with bucket_start(b) <= g.
+__device__ __forceinline__ uint32_t bucket_of(const RowSmem& sm, const ListInfo& L, uint32_t lo, uint32_t hi,
+                                              uint32_t g) {
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (bucket_start(sm, L, mid) <= g) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// The n keys of bucket b sorted descending into LDS (sm.list) or, above LCAP / 2 keys, the
+// row's sort scratch; every thread calls it and gets the buffer.
+__device__ __forceinline__ const uint64_t* sort_event_bucket(const ListInfo& L, uint32_t b, uint64_t* gscratch,
+                                                             RowSmem& sm) {
+    const int tid = threadIdx.x;
+    const uint32_t n = sm.bcnt[b], o0 = sm.boff[b];
+    if (n <= (uint32_t)(2 * BLOCK)) {
+        // ranks by counting (keys are distinct), from a copy in the list's upper half
+        uint64_t* src = sm.list + LCAP / 2;
+        for (uint32_t j = (uint32_t)tid; j < n; j += BLOCK) src[j] = L.G[o0 + j];
+        __syncthreads();
+        const uint32_t i0 = (uint32_t)tid, i1 = (uint32_t)tid + BLOCK;
+        const uint64_t k0 = i0 < n ? src[i0] : ~0ull;
+        const uint64_t k1 = i1 < n ? src[i1] : ~0ull;
+        uint32_t r0 = 0, r1 = 0;
+#pragma unroll 4
+        for (uint32_t j = 0; j < n; j++) {
+            const uint64_t kj = src[j];
+            r0 += kj > k0 ? 1u : 0u;
+            r1 += kj > k1 ? 1u : 0u;
+        }
+        if (i0 < n) sm.list[r0] = k0;
+        if (i1 < n) sm.list[r1] = k1;
+        __syncthreads();
+        return sm.list;
+    }
+    const uint64_t* buf = sm.list;
+    if (wave_id() == 0) {
+        int n2 = WAVE;
+        while ((uint32_t)n2 < n) n2 <<= 1;
+        buf = sort_bucket(gscratch, L.G + o0, n, n2);
+    }
+    __syncthreads();
+    int n2 = WAVE;
+    while ((uint32_t)n2 < n) n2 <<= 1;
+    return n2 <= LCAP ? sm.list : gscratch;
+}
+
+__device__ __noinline__ WalkOut walk_big(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
+                                            uint64_t* gscratch) {
+    RowSmem& sm = g_sm;
+    const int tid = threadIdx.x;
+    uint32_t* const tq = sm.bfill;           // per thread: exclusive unit prefix of its keys
+    uint32_t* const tc = sm.bfill + BLOCK;   // per thread: exclusive rank prefix
+    static_assert(2 * BLOCK <= NB, "per-thread prefixes in the fill counters");
+    WalkState w;
+    walk_set(w, 0.0f, th);
+    w.r = 0;
+    WalkOut o{0.0f, 0u, 0ull, 0};
+    bool stopped = false;
+    uint32_t b0 = 0;
+    while (b0 < L.nb && !stopped) {
+        // the round's buckets [b0, b1): whole buckets within one tile, at least one
+        const uint32_t e0 = sm.boff[b0];
+        uint32_t b1 = bucket_of(sm, L, b0, L.nb + 1, e0 + WTILE);
+        if (b1 <= b0) b1 = b0 + 1;
+        const uint32_t e1 = bucket_start(sm, L, b1);
+        // sub-tiles (more than one only for a single bucket larger than a tile)
+        uint32_t qacc = 0, cacc = 0, first = 0xFFFFFFFFu;
+        for (uint32_t s0 = e0; s0 < e1 && first == 0xFFFFFFFFu; s0 += WTILE) {
+            const uint32_t j0 = s0 + (uint32_t)tid * WPT;
+            uint32_t q[WPT], Q = 0, Cn = 0, tb = 0;
+#pragma unroll
+            for (int i = 0; i < WPT; i++) {
+                const uint32_t j = j0 + (uint32_t)i;
+                const uint64_t key = j < e1 ? L.G[j] : 0ull;
+                const bool valid = key != 0ull && key != excl;
+                const float t = units_of(key_p(key, idxmode), w.ue);
+                q[i] = valid ? quant_units(t) : 0u;
+                tb |= (valid && quant_tie(t)) ? 1u << i : 0u;
+                tb |= valid ? 1u << (16 + i) : 0u;
+                Q = sat_add(Q, q[i]);
+                Cn += valid ? 1u : 0u;
+            }
+            uint32_t Qt, Ct;
+            const uint32_t Qx = sat_add(qacc, block_excl_scan_sat(Q, Qt, sm));
+            const uint32_t Cx = cacc + block_excl_scan<uint32_t>(Cn, sm.wu2, Ct);
+            if (tid < BLOCK) {
+                tq[tid] = Qx;
+                tc[tid] = Cx;
+            }
+            // this thread's first event
+            uint32_t run = sat_add(w.m, Qx), rk = w.r + Cx, mine = 0xFFFFFFFFu;
+#pragma unroll
+            for (int i = 0; i < WPT; i++) {
+                const bool valid = (tb >> (16 + i)) & 1u;
+                run = sat_add(run, q[i]);
+                rk += valid ? 1u : 0u;
+                const bool ev = valid && (((tb >> i) & 1u) || run >= M_TOP || run >= w.tu || rk >= R);
+                if (ev && mine == 0xFFFFFFFFu) mine = j0 + (uint32_t)i;
+            }
+            first = block_min_u(mine, sm.wu);
+            qacc = sat_add(qacc, Qt);
+            cacc += Ct;
+        }
+        if (first == 0xFFFFFFFFu) {  // no event: every bucket of the round added whole
+            w.m = sat_add(w.m, qacc);
+            w.r += cacc;
+            b0 = b1;
+            continue;
+        }
+        // the event's bucket and the state at its start
+        const uint32_t bs = bucket_of(sm, L, b0, b1, first);
+        const uint32_t es = sm.boff[bs];
+        if (bs > b0) {
+            // (one sub-tile: the owner of key es adds its keys before es to its prefix)
+            const uint32_t own = (es - e0) / WPT, skip = (es - e0) % WPT;
+            if ((uint32_t)tid == own) {
+                uint32_t qq = tq[own], cc = tc[own];
+                for (uint32_t i = 0; i < skip; i++) {
+                    const uint64_t key = L.G[e0 + own * WPT + i];
+                    const bool valid = key != 0ull && key != excl;
+                    qq = sat_add(qq, valid ? quant_units(units_of(key_p(key, idxmode), w.ue)) : 0u);
+                    cc += valid ? 1u : 0u;
+                }
+                sm.misc[MS_NFB] = qq;
+                sm.misc[MS_NV] = cc;
+            }
+            __syncthreads();
+            w.m = sat_add(w.m, sm.misc[MS_NFB]);
+            w.r += sm.misc[MS_NV];
+            __syncthreads();
+        }
+        // the bucket sorted, then walked element by element from that state (wave 0)
+        const uint64_t* buf = sort_event_bucket(L, bs, gscratch, sm);
+        const uint32_t n = sm.bcnt[bs];
+        if (wave_id() == 0) {
+            const int lane = lane_id();
+            for (uint32_t j = 0; j < n && !stopped; j += WAVE)
+                stopped = walk_elems(w, j + (uint32_t)lane < n ? buf[j + lane] : 0ull, th, R, excl, idxmode, o, nullptr);
+            if (lane == 0) {
+                sm.misc[MS_FLAG] = stopped ? 1u : 0u;
+                sm.misc[MS_STOP] = o.rank;
+                sm.misc[MS_STOPLO] = (uint32_t)o.key;
+                sm.misc[MS_TOK] = (uint32_t)(o.key >> 32);
+                sm.misc[MS_KIND] = (uint32_t)o.how;
+                sm.mf[MF_CUM] = o.cum;
+                sm.misc[MS_CLO] = w.m;
+                sm.misc[MS_CHI] = (uint32_t)w.ue;
+                sm.misc[MS_CNEXT] = w.tu;
+                sm.misc[MS_VERDICT] = w.r;
+            }
+        }
+        __syncthreads();
+        stopped = sm.misc[MS_FLAG] != 0u;
+        o.rank = sm.misc[MS_STOP];
+        o.key = ((uint64_t)sm.misc[MS_TOK] << 32) | sm.misc[MS_STOPLO];
+        o.how = (int)sm.misc[MS_KIND];
+        o.cum = sm.mf[MF_CUM];
+        w.m = sm.misc[MS_CLO];
+        w.ue = (int32_t)sm.misc[MS_CHI];
+        w.tu = sm.misc[MS_CNEXT];
+        w.r = sm.misc[MS_VERDICT];
+        __syncthreads();
+        b0 = bs + 1;
+    }
+    if (!stopped) {
+        o.cum = state_value(w.m, w.ue);
+        o.rank = w.r;
+        o.key = 0;
+        o.how = 0;
+    }
+    return o;
+}
+
+// The walk: over a small (sorted) list or a bucketed list in LDS by wave 0, the result
+// broadcast through LDS to every thread; over a bucketed list in the spill area (more keys
+// than LDS holds) by the block (walk_big).
 __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
                                      uint64_t* gscratch, float* cum = nullptr) {
+    if (!L.small && L.n > (uint32_t)LCAP) return walk_big(L, th, R, excl, idxmode, gscratch);
     RowSmem& sm = g_sm;
     WalkOut o{0.0f, 0u, 0ull, 0};
     if (wave_id() == 0) {
@@ -1084,6 +1281,7 @@ __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, 
         bool stopped = false;
         for (uint32_t j0 = 0; L.small && j0 < L.n && !stopped; j0 += WAVE)
             stopped = walk_elems(w, j0 + (uint32_t)lane < L.n ? L.G[j0 + lane] : 0ull, th, R, excl, idxmode, o, cum);
+        // a bucketed list in LDS: 64 buckets a step, each lane summing one bucket
         uint32_t b0 = 0;
         while (!L.small && b0 < L.nb && !stopped) {
             const uint32_t b = b0 + (uint32_t)lane;

@@ -29,19 +29,23 @@ struct __align__(16) StreamSmem {
     uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids, two 16-bit halves a word;
                                  // then the histogram (HBINS words); the row finisher's grids
 };
-static_assert(HBINS <= CHUNK_MAX / 2, "the histogram reuses the count array");
+static_assert(2 * HBINS <= CHUNK_MAX / 2, "the histogram reuses the count array");
 
+constexpr int HB_CBITS = 20;              // histogram bins: count bits (a chunk holds at most 8192)
+static_assert(CHUNK_MAX < (1 << HB_CBITS), "bin counts");
 constexpr int NGRID = 512;                // gather-bound grid: bounds -g/8 log2-units, g < NGRID
 constexpr double MFIX = 1099511627776.0;  // 2^40: fixed point of the grid masses
 static_assert(NGRID * 3 <= CHUNK_MAX / 2, "the grids reuse the count array");
 
-// The candidate bound from the chunks' histograms: bin j of chunk c holds the elements
-// j/8 .. (j+1)/8 log2-units below the chunk maximum xm_c, which lies o_c = (xmax - xm_c)
-// log2(e) / T below the row's. On a grid of bounds theta_g = -g/8 (log2-units of
-// exp(s - M)) the bins entirely above theta_g give lower bounds on the count and on the
-// mass of the elements above it; the bound is the highest theta_g whose lower bounds reach
-// k (top-k) or the top-p share of an upper bound on the normalizer with margins for the
-// reference's rounding (sample.rs:392-409). Every kept element lies above it.
+// The candidate bound from the chunks' histograms: bin j of chunk c holds the count and the
+// mass (terms relative to the chunk maximum) of the elements j/4 .. (j+1)/4 log2-units below
+// the chunk maximum xm_c, which lies o_c = (xmax - xm_c) log2(e) / T below the row's. On a
+// grid of bounds theta_g = -g/8 (log2-units of exp(s - M)) the bins entirely above theta_g
+// give lower bounds on the count and on the mass of the elements above it (the masses
+// lowered for the estimates' and the f32 accumulation's errors); the bound is the highest
+// theta_g whose lower bounds reach k (top-k) or the top-p share of an upper bound on the
+// normalizer with margins for the reference's rounding (sample.rs:392-409). Every kept
+// element lies above it.
 __device__ __forceinline__ float gather_bound(const KArgs& a, StreamSmem& sm, const RowCtx& C, float xmax,
                                               double S_hi) {
     const int tid = threadIdx.x;
@@ -54,29 +58,34 @@ __device__ __forceinline__ float gather_bound(const KArgs& a, StreamSmem& sm, co
     }
     __syncthreads();
     const float eps = 0x1p-8f;
-    // the chunks' histograms, 16 words per thread in flight together
+    // the chunks' histograms, 16 bins per thread in flight together
     constexpr int PER = 16;
-    const uint32_t* vh = a.vhist + (int64_t)C.row * nc * HBINS;
+    const uint32_t* vh = a.vhist + (int64_t)C.row * nc * 2 * HBINS;
     for (int b0 = 0; b0 < nc * HBINS; b0 += PER * BLOCK) {
-        uint32_t hv[PER];
+        uint64_t hv[PER];
 #pragma unroll
         for (int r = 0; r < PER; r++) {
             const int idx = b0 + r * BLOCK + tid;
-            hv[r] = (idx < nc * HBINS && (idx % HBINS) != HBINS - 1) ? ld_dev(vh + idx) : 0u;
+            hv[r] = (idx < nc * HBINS && (idx % HBINS) != HBINS - 1)
+                        ? ld_dev64(reinterpret_cast<const uint64_t*>(vh) + idx)
+                        : 0ull;
         }
 #pragma unroll
         for (int r = 0; r < PER; r++) {
-            const uint32_t cnt = hv[r];
-            if (!cnt) continue;
+            const uint32_t cnt = C.kmode ? (uint32_t)(hv[r] & ((1u << HB_CBITS) - 1u)) : 0u;
+            const float ms = C.pmode ? (float)(hv[r] >> HB_CBITS) * 0x1p-24f : 0.0f;
+            if (!cnt && !(ms > 0.0f)) continue;
             const int idx = b0 + r * BLOCK + tid;
             const int c = idx / HBINS, j = idx % HBINS;
             const float o = (xmax - sm.xm[c]) * C.rTl;
-            const float glo = ceilf(8.0f * o + (float)(j + 1) + 8.0f * eps);
+            const float glo = ceilf(8.0f * o + (float)(8 * (j + 1) / HBIN_PER_LOG2) + 8.0f * eps);
             if (glo < (float)NGRID) {
                 const int g = (int)glo;
-                lds_add(&CL[g], cnt);
-                const double m = (double)cnt * exp2(-(double)o - (double)(j + 1) / 8.0 - (double)eps);
-                lds_add64(&ML[g], (uint64_t)(m * MFIX));
+                if (cnt) lds_add(&CL[g], cnt);
+                if (ms > 0.0f) {
+                    const double m = (double)ms * exp2(-(double)o - (double)eps) * (1.0 - 0x1p-9);
+                    lds_add64(&ML[g], (uint64_t)(m * MFIX));
+                }
             }
         }
     }
@@ -352,7 +361,7 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
     const bool want_hist = !C.greedy && (C.kmode || C.pmode) && !(C.min_p >= 0x1p-10f) && a.vhist != nullptr;
     if (want_hist) {
         if (C.prepen) __syncthreads();
-        for (int i = tid; i < HBINS; i += BLOCK) sm.hc[i] = 0u;
+        for (int i = tid; i < 2 * HBINS; i += BLOCK) sm.hc[i] = 0u;
     }
     __syncthreads();
     float lm = sm.wm[0];
@@ -382,22 +391,29 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
         part.xm = lm;
     }
     if (want_hist) {
-        // bin j: the element lies j/8 .. (j+1)/8 log2-units below the chunk maximum; the
-        // elements further down (most of them) and the masked ones are not counted
+        // bin j: the element lies j/4 .. (j+1)/4 log2-units below the chunk maximum; its
+        // count and (top-p rows) its term 2^((x - xm) log2(e) / T) go there; the elements
+        // further down and the masked ones are not counted.
+        // one 64-bit add per element: the count in the low HB_CBITS bits, the term in fixed
+        // point (2^-24 units of the chunk maximum's, truncated: a lower bound) above them
         if (lm > -__builtin_inff()) {
-            const float sc = C.rTl * (float)HBIN_PER_LOG2;
+            uint64_t* hb = reinterpret_cast<uint64_t*>(sm.hc);
+            const bool pm = C.pmode;
 #pragma unroll
             for (int q = 0; q < VEC; q++)
 #pragma unroll
                 for (int e = 0; e < EPV; e++) {
-                    const float xv = x[q][e];
-                    const float f = (lm - xv) * sc;
-                    if (f < (float)(HBINS - 1)) lds_add(&sm.hc[(uint32_t)f], 1u);
+                    const float d = (x[q][e] - lm) * C.rTl;
+                    const float f = -d * (float)HBIN_PER_LOG2;
+                    if (f < (float)(HBINS - 1)) {
+                        const uint32_t fx = pm ? (uint32_t)(__builtin_amdgcn_exp2f(d) * 16777216.0f) : 0u;
+                        lds_add64(&hb[(uint32_t)f], ((uint64_t)fx << HB_CBITS) | 1u);
+                    }
                 }
         }
         __syncthreads();
-        uint32_t* dst = a.vhist + ((int64_t)row * a.n_chunks + chunk) * HBINS;
-        for (int i = tid; i < HBINS; i += BLOCK) st_dev(dst + i, sm.hc[i]);
+        uint32_t* dst = a.vhist + ((int64_t)row * a.n_chunks + chunk) * 2 * HBINS;
+        for (int i = tid; i < 2 * HBINS; i += BLOCK) st_dev(dst + i, sm.hc[i]);
     }
     if (tid < 4) {
         const uint64_t* pw = reinterpret_cast<const uint64_t*>(&part);
