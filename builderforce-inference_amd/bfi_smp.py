@@ -75,7 +75,7 @@ def lib():
         L.bfi_draft.restype = ctypes.c_size_t
         L.bfi_parse_id_union.argtypes = [ctypes.c_char_p, I64, P]
         L.bfi_parse_id_union.restype = I32
-        L.bfi_spec_replay.argtypes = [P, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32, I64, ctypes.c_size_t,
+        L.bfi_spec_replay.argtypes = [P, P, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32, I64, ctypes.c_size_t,
                                       ctypes.c_size_t, P, P, P, P, P, P]
         # allow-mask producer (include/bfi_mask.h)
         L.bfi_mask_create.argtypes = [I32, ctypes.POINTER(P)]
@@ -155,13 +155,16 @@ def parse_id_union(grammar: str, n_vocab: int):
     return m[: (n_vocab + 31) // 32] if ok else None
 
 
-def spec_replay(drafted, kernel_accepted, kernel_next, eos, generated, max_tokens, rng_state):
+def spec_replay(drafted, kernel_accepted, kernel_next, eos, generated, max_tokens, rng_state, closes_tool=None):
+    """bfi_spec_replay; closes_tool: per draft, whether appending it completes a tool call."""
     d = np.ascontiguousarray(drafted, dtype=np.uint32)
+    stops = None if closes_tool is None else np.ascontiguousarray(closes_tool, dtype=np.uint8)
     pushed = np.zeros(max(d.size, 1), np.uint32)
     st = ctypes.c_uint64(rng_state)
     n_pushed, acc = ctypes.c_size_t(0), ctypes.c_size_t(0)
     done, pend = ctypes.c_int(0), ctypes.c_int64(0)
-    rc = lib().bfi_spec_replay(_np_ptr(d), d.size, kernel_accepted, kernel_next, -1 if eos is None else eos,
+    rc = lib().bfi_spec_replay(_np_ptr(d), None if stops is None else _np_ptr(stops), d.size, kernel_accepted,
+                               kernel_next, -1 if eos is None else eos,
                                generated, max_tokens, ctypes.byref(st), _np_ptr(pushed), ctypes.byref(n_pushed),
                                ctypes.byref(acc), ctypes.byref(done), ctypes.byref(pend))
     if rc:

@@ -690,7 +690,6 @@ __device__ __noinline__ StreamOut row_stream(const StreamArgs Ain) {
     constexpr int EPV = Elem<BF16>::EPV;
     constexpr int NV = BF16 ? RNV_BF16 : RNV_F32;
     constexpr uint32_t SPAN = (uint32_t)BLOCK * NV * EPV;
-    const int tid = threadIdx.x;
     const uint32_t hi = A.hi;
     const float rS = A.kind ? 1.0f / A.S : 0.0f;
     StreamRun R;
@@ -1126,16 +1125,11 @@ __device__ __forceinline__ const uint64_t* sort_event_bucket(const ListInfo& L, 
         __syncthreads();
         return sm.list;
     }
-    const uint64_t* buf = sm.list;
-    if (wave_id() == 0) {
-        int n2 = WAVE;
-        while ((uint32_t)n2 < n) n2 <<= 1;
-        buf = sort_bucket(gscratch, L.G + o0, n, n2);
-    }
-    __syncthreads();
     int n2 = WAVE;
     while ((uint32_t)n2 < n) n2 <<= 1;
-    return n2 <= LCAP ? sm.list : gscratch;
+    if (wave_id() == 0) (void)sort_bucket(gscratch, L.G + o0, n, n2);
+    __syncthreads();
+    return n2 <= LCAP ? sm.list : gscratch;  // (sort_bucket's buffer)
 }
 
 __device__ __noinline__ WalkOut walk_big(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,

@@ -1,6 +1,8 @@
 // bfi_host.cpp — host-side helpers of the C ABI and the C++ mirror (bfi_host.hpp).
 #include "bfi_host.hpp"
 
+#include "bfi_grammar.hpp"
+
 #include <cstring>
 
 extern "C" {
@@ -46,59 +48,11 @@ size_t bfi_draft(const uint32_t* ctx, size_t len, size_t k, size_t ngram_max, si
 
 }  // extern "C"
 
-namespace {
-
-bool ws(char c) { return c == ' ' || c == '\t' || c == '\n' || c == '\r' || c == '\v' || c == '\f'; }
-
-std::string_view trim(std::string_view s) {
-    while (!s.empty() && ws(s.front())) s.remove_prefix(1);
-    while (!s.empty() && ws(s.back())) s.remove_suffix(1);
-    return s;
-}
-
-bool strip(std::string_view& s, std::string_view pre) {
-    if (s.substr(0, pre.size()) != pre) return false;
-    s.remove_prefix(pre.size());
-    return true;
-}
-
-// Rust `str::parse::<u32>()`: optional '+', ASCII digits, no overflow.
-bool parse_u32(std::string_view s, uint32_t& v) {
-    if (!s.empty() && s.front() == '+') s.remove_prefix(1);
-    if (s.empty()) return false;
-    uint64_t x = 0;
-    for (char c : s) {
-        if (c < '0' || c > '9') return false;
-        x = x * 10 + (uint64_t)(c - '0');
-        if (x > 0xFFFFFFFFull) return false;
-    }
-    v = (uint32_t)x;
-    return true;
-}
-
-}  // namespace
-
 extern "C" int bfi_parse_id_union(const char* grammar, int64_t n_vocab, uint32_t* mask_out) {
-    // sample.rs:207-221 parse_id_union, 231-235 strip_root
+    // sample.rs:207-221 parse_id_union, 231-235 strip_root (Unicode str::trim)
     if (!grammar || n_vocab < 0 || (n_vocab > 0 && !mask_out)) return 0;
-    std::string_view s = trim(grammar);
-    if (!strip(s, "root")) return 0;
-    s = trim(s);
-    if (!strip(s, "::=")) return 0;
-    s = trim(s);
     std::vector<uint32_t> ids;
-    for (;;) {
-        size_t bar = s.find('|');
-        std::string_view part = trim(s.substr(0, bar));
-        if (!strip(part, "id(") || part.empty() || part.back() != ')') return 0;
-        part.remove_suffix(1);
-        uint32_t id;
-        if (!parse_u32(trim(part), id)) return 0;
-        ids.push_back(id);
-        if (bar == std::string_view::npos) break;
-        s.remove_prefix(bar + 1);
-    }
-    if (ids.empty()) return 0;
+    if (!bfig::parse_id_union(grammar, &ids)) return 0;
     const size_t words = (size_t)((n_vocab + 31) / 32);
     std::memset(mask_out, 0, words * sizeof(uint32_t));
     for (uint32_t id : ids)
@@ -149,7 +103,8 @@ void Sampler::sample_rows(const void* d_logits, int dtype, int64_t n_rows, int64
 }
 
 SpecReplay replay_spec(const std::vector<uint32_t>& drafted, int32_t kernel_accepted, uint32_t kernel_next,
-                       std::optional<uint32_t> eos, size_t generated, size_t max_tokens, Rng& rng) {
+                       std::optional<uint32_t> eos, size_t generated, size_t max_tokens, Rng& rng,
+                       const std::vector<bool>& closes_tool) {
     // spec.rs:140-162 with the verdicts already computed on the GPU
     SpecReplay r;
     std::optional<uint32_t> correction;
@@ -167,6 +122,10 @@ SpecReplay replay_spec(const std::vector<uint32_t>& drafted, int32_t kernel_acce
         }
         r.pushed.push_back(d);
         r.accepted++;
+        if (i < closes_tool.size() && closes_tool[i]) {  // Pushed::Stopped (spec.rs:150-153)
+            r.done = true;
+            break;
+        }
         if (generated + r.pushed.size() >= max_tokens) {  // budget_spent
             r.done = true;
             break;
@@ -179,17 +138,19 @@ SpecReplay replay_spec(const std::vector<uint32_t>& drafted, int32_t kernel_acce
 }  // namespace bfi
 
 // C entry point of replay_spec for callers without C++ (and the CPU tests).
-extern "C" int bfi_spec_replay(const uint32_t* drafted, size_t n_drafted, int32_t kernel_accepted,
-                               uint32_t kernel_next, int64_t eos, size_t generated, size_t max_tokens,
-                               uint64_t* rng_state, uint32_t* pushed_out, size_t* n_pushed, size_t* accepted,
-                               int* done, int64_t* pending) {
+extern "C" int bfi_spec_replay(const uint32_t* drafted, const uint8_t* closes_tool, size_t n_drafted,
+                               int32_t kernel_accepted, uint32_t kernel_next, int64_t eos, size_t generated,
+                               size_t max_tokens, uint64_t* rng_state, uint32_t* pushed_out, size_t* n_pushed,
+                               size_t* accepted, int* done, int64_t* pending) {
     if ((n_drafted && !drafted) || !rng_state || !pushed_out || !n_pushed || !accepted || !done || !pending)
         return BFI_SMP_EINVAL;
     std::vector<uint32_t> d(drafted, drafted + n_drafted);
+    std::vector<bool> stops;
+    if (closes_tool) stops.assign(closes_tool, closes_tool + n_drafted);
     bfi::Rng rng(*rng_state);
     std::optional<uint32_t> e;
     if (eos >= 0) e = (uint32_t)eos;
-    bfi::SpecReplay r = bfi::replay_spec(d, kernel_accepted, kernel_next, e, generated, max_tokens, rng);
+    bfi::SpecReplay r = bfi::replay_spec(d, kernel_accepted, kernel_next, e, generated, max_tokens, rng, stops);
     *rng_state = rng.state;
     std::memcpy(pushed_out, r.pushed.data(), r.pushed.size() * sizeof(uint32_t));
     *n_pushed = r.pushed.size();

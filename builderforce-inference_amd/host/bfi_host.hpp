@@ -111,8 +111,11 @@ struct SpecReplay {
 };
 // kernel_accepted / kernel_next: bfi_smp_verify outputs of this sequence. `generated` is
 // how many tokens the slot has generated so far (incl. t0), max_tokens its budget.
+// closes_tool[i] (empty: none): appending drafted[i] completes a tool call, i.e. the
+// caller's should_stop_tool (engine/mod.rs:548) holds for the generated ids through it.
 SpecReplay replay_spec(const std::vector<uint32_t>& drafted, int32_t kernel_accepted, uint32_t kernel_next,
-                       std::optional<uint32_t> eos, size_t generated, size_t max_tokens, Rng& slot_rng);
+                       std::optional<uint32_t> eos, size_t generated, size_t max_tokens, Rng& slot_rng,
+                       const std::vector<bool>& closes_tool = {});
 
 // mix_decode (engine/mod.rs:560-580): every live sequence takes one step per round;
 // returns the number of shared rounds.

@@ -212,14 +212,18 @@ size_t bfi_draft(const uint32_t *ctx_ids, size_t len, size_t k, size_t ngram_max
 int bfi_parse_id_union(const char *grammar, int64_t n_vocab, uint32_t *mask_out);
 
 /* Host half of take_token_spec after a GPU verify (spec.rs:140-179): replays the stop
- * rules (EOS never appended, budget `max_tokens` counting `generated` tokens so far) over
- * the kernel's verdicts for one sequence and advances the slot RNG by two draws per judged
- * row. eos < 0 means no EOS id. Outputs: pushed ids, accepted count (SpecStats::accepted),
- * done flag, pending correction (-1 = none). */
-int bfi_spec_replay(const uint32_t *drafted, size_t n_drafted, int32_t kernel_accepted,
-                    uint32_t kernel_next, int64_t eos, size_t generated, size_t max_tokens,
-                    uint64_t *rng_state, uint32_t *pushed_out, size_t *n_pushed, size_t *accepted,
-                    int *done, int64_t *pending);
+ * rules of push_token (engine/mod.rs:451-462) over the kernel's verdicts for one sequence
+ * and advances the slot RNG by two draws per judged row. Rules: an EOS draft is never
+ * appended and ends the slot (Pushed::Eos); a draft with closes_tool[i] != 0 is appended,
+ * counted and ends the slot (Pushed::Stopped, spec.rs:150-153) — the caller evaluates
+ * should_stop_tool (engine/mod.rs:548) on the generated ids through drafted[i];
+ * closes_tool may be NULL (no draft closes a tool call); the budget `max_tokens` counts
+ * `generated` tokens so far. eos < 0 means no EOS id. Outputs: pushed ids, accepted count
+ * (SpecStats::accepted), done flag, pending correction (-1 = none). */
+int bfi_spec_replay(const uint32_t *drafted, const uint8_t *closes_tool, size_t n_drafted,
+                    int32_t kernel_accepted, uint32_t kernel_next, int64_t eos, size_t generated,
+                    size_t max_tokens, uint64_t *rng_state, uint32_t *pushed_out, size_t *n_pushed,
+                    size_t *accepted, int *done, int64_t *pending);
 
 #ifdef __cplusplus
 } /* extern "C" */

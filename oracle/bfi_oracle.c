@@ -380,13 +380,41 @@ size_t orc_draft(const uint32_t *ctx, size_t len, size_t k, size_t ngram_max, si
 
 /* ---- parse_id_union: sample.rs:207-221, strip_root 231-235 --------------------------- */
 
-static int is_ws(char c) { /* char::is_whitespace restricted to ASCII */
-    return c == ' ' || c == '\t' || c == '\n' || c == '\r' || c == '\v' || c == '\f';
+/* char::is_whitespace: the Unicode White_Space property (Rust core's table). */
+static int is_white_space(uint32_t cp) {
+    switch (cp) {
+    case 0x09: case 0x0A: case 0x0B: case 0x0C: case 0x0D: case 0x20: case 0x85: case 0xA0:
+    case 0x1680: case 0x2028: case 0x2029: case 0x202F: case 0x205F: case 0x3000:
+        return 1;
+    default:
+        return cp >= 0x2000 && cp <= 0x200A;
+    }
 }
 
+/* The code point encoded at s (UTF-8; s < e) and its byte length. */
+static uint32_t utf8_at(const char *s, const char *e, int *len) {
+    const unsigned char c = (unsigned char)s[0];
+    int n = 1;
+    uint32_t cp = c;
+    if (c >= 0xF0) { n = 4; cp = c & 0x07; }
+    else if (c >= 0xE0) { n = 3; cp = c & 0x0F; }
+    else if (c >= 0xC0) { n = 2; cp = c & 0x1F; }
+    if (e - s < n) { *len = 1; return c; }
+    for (int i = 1; i < n; i++) cp = (cp << 6) | ((unsigned char)s[i] & 0x3F);
+    *len = n;
+    return cp;
+}
+
+/* str::trim: White_Space code points off both ends. */
 static void trim(const char **s, const char **e) {
-    while (*s < *e && is_ws(**s)) (*s)++;
-    while (*e > *s && is_ws((*e)[-1])) (*e)--;
+    int n;
+    while (*s < *e && is_white_space(utf8_at(*s, *e, &n))) *s += n;
+    while (*e > *s) {
+        const char *p = *e - 1;
+        while (p > *s && (((unsigned char)*p) & 0xC0) == 0x80) p--; /* the last code point's start */
+        if (!is_white_space(utf8_at(p, *e, &n)) || p + n != *e) break;
+        *e = p;
+    }
 }
 
 static int starts(const char *s, const char *e, const char *pre) {

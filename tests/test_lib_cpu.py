@@ -64,20 +64,56 @@ def test_draft_matches_reference_kats_and_oracle():
         assert bfi_smp.draft(c, k, nmax, nmin) == O.draft(c, k, nmax, nmin)
 
 
-def test_parse_id_union_matches_oracle():
+# Rust's str::trim strips Unicode White_Space (sample.rs:231-235); code points a Rust
+# program does not treat as whitespace (U+200B, U+180E, U+FEFF, the C0 separators U+001C..
+# U+001F that Python's str.isspace accepts) must stay.
+_WS_IN = ["\u00a0", "\u3000", "\u2028", "\u2029", "\u0085", "\u1680", "\u2000", "\u200a", "\u202f", "\u205f",
+          "\x0b", "\x0c", "\t\u3000\n"]
+_WS_OUT = ["\u200b", "\u180e", "\ufeff", "\x1c", "\x1f", "\u2060"]
+
+
+def _id_union_cases():
     cases = ["root ::= id(1)", "  root ::=  id( 3 ) | id(+7)|id(0)  ", "root ::= id(1) | foo", 'root ::= "ab"',
              "root::=id(5)", "root ::= ", "root ::= id(4294967295)", "root ::= id(4294967296)", "rootx ::= id(1)",
              "root ::= id(70) | id(2)"]
-    for g in cases:
+    for w in _WS_IN + _WS_OUT:
+        cases += [f"root ::= id(7){w}", f"{w}root ::= id(7)", f"root{w}::={w}id(7){w}|{w}id(9)",
+                  f"root ::= id({w}12{w})", f"{w}{w}root ::= id(3) |id(4){w}{w}"]
+    return cases
+
+
+def test_parse_id_union_unicode_trim_matches_the_python_restatement():
+    """bfi_parse_id_union and the C oracle against constraint.parse_id_union, whose trim is
+    an independent statement of Rust's White_Space set."""
+    import constraint as K
+    for g in _id_union_cases():
+        want = K.parse_id_union(g)
         a = bfi_smp.parse_id_union(g, 64)
         b = O.parse_id_union(g, 64)
-        assert (a is None) == (b is None), g
+        for got, who in ((a, "library"), (b, "oracle")):
+            assert (got is None) == (want is None), (who, repr(g))
+            if want is not None:
+                ids = {i for i in range(64) if (int(got[i >> 5]) >> (i & 31)) & 1}
+                assert ids == {i for i in want if i < 64}, (who, repr(g))
+    # the whitespace set decides: these are id unions only with Rust's trim
+    assert K.parse_id_union("root ::= id(7)\u3000") == {7}
+    assert K.parse_id_union("root ::= id(7)\u200b") is None
+
+
+def test_parse_id_union_matches_oracle():
+    for g in _id_union_cases():
+        a = bfi_smp.parse_id_union(g, 64)
+        b = O.parse_id_union(g, 64)
+        assert (a is None) == (b is None), repr(g)
         if a is not None:
-            assert np.array_equal(a, b), g
+            assert np.array_equal(a, b), repr(g)
 
 
-def _py_replay(drafted, acc, nxt, eos, generated, max_tokens, rng_state):
-    """spec.rs:140-179 stop rules, restated for the comparison."""
+def _py_replay(drafted, acc, nxt, eos, generated, max_tokens, rng_state, stops=None):
+    """spec.rs:137-179 with push_token's rules (engine/mod.rs:451-462), restated for the
+    comparison: two draws per judged draft; Reject -> correction; Eos -> done, not appended;
+    Stopped (the draft completes a tool call) -> appended, counted, done; Continue ->
+    appended, counted, then the budget."""
     pushed, accepted, done, correction = [], 0, False, None
     st = rng_state
     for i, d in enumerate(drafted):
@@ -90,6 +126,10 @@ def _py_replay(drafted, acc, nxt, eos, generated, max_tokens, rng_state):
             done = True
             break
         pushed.append(d)
+        if stops is not None and stops[i]:
+            accepted += 1
+            done = True
+            break
         accepted += 1
         if generated + len(pushed) >= max_tokens:
             done = True
@@ -99,7 +139,7 @@ def _py_replay(drafted, acc, nxt, eos, generated, max_tokens, rng_state):
 
 def test_spec_replay_matches_stop_rules():
     rng = np.random.default_rng(11)
-    for _ in range(400):
+    for _ in range(600):
         n = int(rng.integers(0, 6))
         drafted = rng.integers(0, 5, n).tolist()
         acc = int(rng.integers(0, n + 1))
@@ -108,9 +148,33 @@ def test_spec_replay_matches_stop_rules():
         gen = int(rng.integers(1, 8))
         mx = gen + int(rng.integers(0, 6))
         st = int(rng.integers(0, 2**63))
-        got = bfi_smp.spec_replay(drafted, acc, nxt, eos, gen, mx, st)
-        want = _py_replay(drafted, acc, nxt, eos, gen, mx, st)
+        stops = None if rng.random() < 0.4 else (rng.random(n) < 0.3).tolist()
+        got = bfi_smp.spec_replay(drafted, acc, nxt, eos, gen, mx, st, stops)
+        want = _py_replay(drafted, acc, nxt, eos, gen, mx, st, stops)
         assert got == want
+
+
+def test_spec_replay_tool_stop_ends_the_slot():
+    """Pushed::Stopped (spec.rs:150-153): the draft that closes a tool call is appended and
+    counted, the slot is done, later accepted drafts are dropped and no correction is
+    pending; an EOS draft is never a stop (push_token checks EOS first)."""
+    st = 12345
+    r = bfi_smp.spec_replay([5, 6, 7, 8], 4, 9, None, 1, 100, st, [0, 1, 0, 0])
+    assert r["pushed"] == [5, 6] and r["accepted"] == 2 and r["done"] and r["pending"] is None
+    # every draft judged up to the stop draws twice: two judged drafts
+    s2 = st
+    for _ in range(4):
+        _, s2 = O.rng_f32(s2)
+    assert r["rng_state"] == s2
+    # rejected before the stop: the correction stands
+    r = bfi_smp.spec_replay([5, 6, 7], 1, 9, None, 1, 100, st, [0, 1, 0])
+    assert r["pushed"] == [5] and not r["done"] and r["pending"] == 9
+    # EOS wins over the stop flag
+    r = bfi_smp.spec_replay([5, 3], 2, 9, 3, 1, 100, st, [0, 1])
+    assert r["pushed"] == [5] and r["accepted"] == 1 and r["done"]
+    # without the flags the old rules hold
+    r = bfi_smp.spec_replay([5, 6, 7, 8], 4, 9, None, 1, 100, st)
+    assert r["pushed"] == [5, 6, 7, 8] and not r["done"] and r["pending"] is None
 
 
 def test_create_without_device_reports_error():
