@@ -1,4 +1,6 @@
-// bfi_host.cpp — host-side helpers of the C ABI and the C++ mirror (bfi_host.hpp).
+// bfi_host.cpp — host-side helpers of the C ABI and the C++ mirror (bfi_host.hpp): Rng,
+// slot_rng, draft, the id-union grammar and the spec replay. No GPU calls (bfi_sampler.cpp
+// holds the Sampler class).
 #include "bfi_host.hpp"
 
 #include "bfi_grammar.hpp"
@@ -74,34 +76,6 @@ std::optional<std::vector<uint32_t>> id_union_mask(const std::string& grammar, i
     return m;
 }
 
-Sampler::Sampler(int device) { check(bfi_smp_create(device, &ctx_)); }
-
-Sampler::~Sampler() { bfi_smp_destroy(ctx_); }
-
-void Sampler::check(int rc) {
-    if (rc != BFI_SMP_OK) throw Error(rc, bfi_smp_last_error(ctx_));
-}
-
-uint32_t Sampler::sample(const float* logits, size_t n_vocab, const uint32_t* prev, size_t n_prev,
-                         const SampleParams& p) {
-    std::optional<std::vector<uint32_t>> mask;
-    if (p.grammar) mask = id_union_mask(*p.grammar, (int64_t)n_vocab);
-    const bfi_smp_row_params row = p.row();
-    const float u = Rng(p.seed).f32();  // sample.rs:307 re-seeds every call
-    uint32_t tok = 0;
-    check(bfi_smp_sample_host(ctx_, logits, (int64_t)n_vocab, prev, (int64_t)n_prev, &row,
-                              mask ? mask->data() : nullptr, u, &tok));
-    return tok;
-}
-
-void Sampler::sample_rows(const void* d_logits, int dtype, int64_t n_rows, int64_t n_vocab, int64_t row_stride,
-                          const bfi_smp_row_params* d_params, const uint32_t* d_hist, const int64_t* d_hist_off,
-                          const uint32_t* d_mask, int64_t mask_stride, const float* d_u, uint32_t* d_out,
-                          void* stream) {
-    check(bfi_smp_sample_rows(ctx_, d_logits, dtype, n_rows, n_vocab, row_stride, d_params, d_hist, d_hist_off,
-                              d_mask, mask_stride, d_u, d_out, stream));
-}
-
 SpecReplay replay_spec(const std::vector<uint32_t>& drafted, int32_t kernel_accepted, uint32_t kernel_next,
                        std::optional<uint32_t> eos, size_t generated, size_t max_tokens, Rng& rng,
                        const std::vector<bool>& closes_tool) {
@@ -152,7 +126,7 @@ extern "C" int bfi_spec_replay(const uint32_t* drafted, const uint8_t* closes_to
     if (eos >= 0) e = (uint32_t)eos;
     bfi::SpecReplay r = bfi::replay_spec(d, kernel_accepted, kernel_next, e, generated, max_tokens, rng, stops);
     *rng_state = rng.state;
-    std::memcpy(pushed_out, r.pushed.data(), r.pushed.size() * sizeof(uint32_t));
+    if (!r.pushed.empty()) std::memcpy(pushed_out, r.pushed.data(), r.pushed.size() * sizeof(uint32_t));
     *n_pushed = r.pushed.size();
     *accepted = r.accepted;
     *done = r.done ? 1 : 0;

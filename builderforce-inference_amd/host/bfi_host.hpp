@@ -75,6 +75,33 @@ struct Error : std::runtime_error {
     Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
 };
 
+// The host half of take_token_spec (spec.rs:137-179) after the GPU verify: applies the stop
+// rules to the kernel's verdicts and advances the slot RNG by two draws per judged row.
+struct SpecReplay {
+    std::vector<uint32_t> pushed;  // tokens appended to all_ids (EOS never appended)
+    size_t accepted = 0;           // counted into SpecStats::accepted
+    bool done = false;             // EOS / tool stop / budget reached
+    std::optional<uint32_t> pending;
+    uint32_t kernel_next = 0;      // verify_step: the kernel's correction or bonus sample
+};
+
+// One sequence of a batched verify step (the GenSlot fields take_token_spec uses).
+struct SpecSeq {
+    std::vector<uint32_t> drafted;  // draft() after t0 (empty: nothing judged)
+    std::vector<bool> closes_tool;  // per draft: appending it completes a tool call
+    Rng rng{0};                     // slot_rng (spec.rs:185-187), advanced by the replay
+    size_t generated = 0;           // tokens generated so far, t0 included
+    size_t max_tokens = 0;
+    float u_bonus = 0.0f;           // Rng(params.seed).f32(): the next pick's uniform
+};
+// kernel_accepted / kernel_next: bfi_smp_verify outputs of this sequence. `generated` is
+// how many tokens the slot has generated so far (incl. t0), max_tokens its budget.
+// closes_tool[i] (empty: none): appending drafted[i] completes a tool call, i.e. the
+// caller's should_stop_tool (engine/mod.rs:548) holds for the generated ids through it.
+SpecReplay replay_spec(const std::vector<uint32_t>& drafted, int32_t kernel_accepted, uint32_t kernel_next,
+                       std::optional<uint32_t> eos, size_t generated, size_t max_tokens, Rng& slot_rng,
+                       const std::vector<bool>& closes_tool = {});
+
 // Owns a bfi_smp_ctx. Not for concurrent use (one per engine thread, like the reference's
 // Mutex<Option<Loaded>>).
 class Sampler {
@@ -94,28 +121,36 @@ class Sampler {
                      const uint32_t* d_mask, int64_t mask_stride, const float* d_u, uint32_t* d_out,
                      void* stream);
 
+    // spec-lookup verify over device rows (engine/spec.rs:137-162, one call for all
+    // sequences; include/bfi_sampler.h bfi_smp_verify).
+    void verify(const void* d_logits, int dtype, int64_t n_seq, int64_t rows_per_seq, int64_t n_vocab,
+                int64_t row_stride, const bfi_smp_row_params* d_params, const uint32_t* d_hist,
+                const int64_t* d_hist_off, const uint32_t* d_drafts, const int32_t* d_draft_len,
+                const uint32_t* d_mask, int64_t mask_stride, const float* d_u_pairs, const float* d_u_bonus,
+                int32_t* d_out_accepted, uint32_t* d_out_next, void* stream);
+
+    // The verify half of take_token_spec for every live sequence at once: after the
+    // caller's forward_each produced rows_per_seq rows per sequence (sequence s: rows
+    // [s * rows_per_seq, s * rows_per_seq + drafted.size()], rows_per_seq > every draft's
+    // length), judges all drafts in one verify call with uniforms from each slot RNG and
+    // replays the stop rules per sequence (advancing the slot RNGs). d_hist / d_hist_off:
+    // each sequence's all_ids before its drafts (t0 included). Synchronizes `stream`.
+    std::vector<SpecReplay> verify_step(const void* d_logits, int dtype, int64_t rows_per_seq,
+                                               int64_t n_vocab, int64_t row_stride,
+                                               const bfi_smp_row_params* d_params, const uint32_t* d_hist,
+                                               const int64_t* d_hist_off, const uint32_t* d_mask,
+                                               int64_t mask_stride, std::vector<SpecSeq>& seqs,
+                                               std::optional<uint32_t> eos, void* stream);
+
     bfi_smp_ctx* ctx() { return ctx_; }
 
   private:
     void check(int rc);
+    void* staging(size_t bytes);  // device staging of verify_step's small arrays
     bfi_smp_ctx* ctx_ = nullptr;
+    void* dbuf_ = nullptr;
+    size_t dcap_ = 0;
 };
-
-// The host half of take_token_spec (spec.rs:137-179) after the GPU verify: applies the stop
-// rules to the kernel's verdicts and advances the slot RNG by two draws per judged row.
-struct SpecReplay {
-    std::vector<uint32_t> pushed;  // tokens appended to all_ids (EOS never appended)
-    size_t accepted = 0;           // counted into SpecStats::accepted
-    bool done = false;             // EOS / tool stop / budget reached
-    std::optional<uint32_t> pending;
-};
-// kernel_accepted / kernel_next: bfi_smp_verify outputs of this sequence. `generated` is
-// how many tokens the slot has generated so far (incl. t0), max_tokens its budget.
-// closes_tool[i] (empty: none): appending drafted[i] completes a tool call, i.e. the
-// caller's should_stop_tool (engine/mod.rs:548) holds for the generated ids through it.
-SpecReplay replay_spec(const std::vector<uint32_t>& drafted, int32_t kernel_accepted, uint32_t kernel_next,
-                       std::optional<uint32_t> eos, size_t generated, size_t max_tokens, Rng& slot_rng,
-                       const std::vector<bool>& closes_tool = {});
 
 // mix_decode (engine/mod.rs:560-580): every live sequence takes one step per round;
 // returns the number of shared rounds.

@@ -645,7 +645,7 @@ void orc_verify_seq(const void *rows, int dtype, int64_t n_vocab, int64_t row_st
     *accepted = 0;
     *next = 0;
     if (!row || !ids || !w || !h) goto done;
-    memcpy(h, hist, n_hist * sizeof(uint32_t));
+    if (n_hist) memcpy(h, hist, n_hist * sizeof(uint32_t));
     for (size_t i = 0; i <= draft_len; i++) {
         row_to_f32(rows, dtype, row_stride, (int64_t)i, n_vocab, row);
         const uint32_t *m = masks ? masks + (int64_t)i * mask_stride : NULL;

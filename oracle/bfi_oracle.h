@@ -20,7 +20,9 @@
  *                                  min-p) + brute force over all params at V <= 8
  *   orc_judge, orc_draft           6 reference KATs (spec.rs:193-256) incl. the Monte-Carlo
  *                                  distribution check
- *   orc_parse_id_union             reference KAT grammar_id_mask_rejects_forbidden_token
+ *   orc_parse_id_union             reference KAT grammar_id_mask_rejects_forbidden_token;
+ *                                  the Unicode White_Space trim (str::trim) against
+ *                                  oracle/constraint.py's independent statement
  *   frequency penalty              parity unpinned: absent in the reference (sample.rs:18-21);
  *                                  this file defines the extension, pinned only by the
  *                                  closed form l - f*count in the tests
