@@ -8,9 +8,11 @@ Pinned by: the reference's constraint tests (sample.rs:505-581, restated as know
 tests/test_oracle_constraint.py); for json_object_prefix_ok, Python's json module on complete
 objects and on every prefix of them, and brute force over all strings of up to six structural
 characters against an independent statement of the scan (strings collapsed by a regular
-expression, the depth as a running sum); for json_name_so_far, tool_call_prefix_ok and the
-grammar parsers, hand-derived cases (the key's restart after a non-colon, escapes, prefixes
-of several names, Rust's whitespace set).
+expression, the depth as a running sum); for json_name_so_far and tool_call_prefix_ok,
+hand-derived cases (the key's restart after a non-colon, escapes, prefixes of several names)
+and brute force over more than 100,000 short strings of the bytes that decide the scan
+against an independent statement (a regular-expression search); for the grammar parsers,
+hand-derived cases and Rust's White_Space set, with and without whitespace on either side.
 """
 from __future__ import annotations
 

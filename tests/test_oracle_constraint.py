@@ -181,3 +181,102 @@ def test_json_object_prefix_ok_brute_force():
             assert K.json_object_prefix_ok(b) == _prefix_ok_independent(b), b
             n += 1
     assert n > 500000
+
+
+# ---- json_name_so_far / tool_call_prefix_ok against an independent statement ------------
+#
+# sample.rs:144-206 as a search over regular expressions rather than a byte loop: every
+# start of `"name"` (overlapping starts included: the closing quote may open the next key),
+# in order; blanks are u8::is_ascii_whitespace (space, \t, \n, \x0c, \r).
+
+import re
+
+_BL = rb"[ \t\n\x0c\r]*"
+_KEY = re.compile(rb'(?="name")')
+_AFTER_KEY = re.compile(_BL + rb"(:?)")
+_VALUE = re.compile(rb"((?:[^\"\\]|\\[\x00-\xff])*)(\\?)(\"?)", re.S)
+
+
+def _name_so_far_independent(b: bytes):
+    for m in _KEY.finditer(b):
+        j = m.start() + 6
+        a = _AFTER_KEY.match(b, j)
+        if a.end() == len(b) and not a.group(1):
+            return ("missing",)  # blanks run to the end: no colon yet
+        if not a.group(1):
+            continue  # not followed by a colon: not the key, keep looking
+        k = re.compile(_BL).match(b, a.end()).end()
+        if k == len(b):
+            return ("partial", b"")
+        if b[k:k + 1] != b'"':
+            return ("invalid",)
+        v = _VALUE.match(b, k + 1)
+        body = v.group(1) + v.group(2)  # a trailing lone backslash stays in the value
+        return ("complete", body) if v.group(3) else ("partial", body)
+    return ("missing",)
+
+
+def _tool_ok_independent(b: bytes, choice: int, named: bytes, names) -> bool:
+    if not _prefix_ok_independent(b):
+        return False
+    if choice not in (K.TOOL_REQUIRED, K.TOOL_NAMED):
+        return True
+    kind, *val = _name_so_far_independent(b)
+    allowed = [named] if choice == K.TOOL_NAMED else list(names)
+    if kind == "missing":
+        return True
+    if kind == "invalid":
+        return False
+    v = val[0]
+    if choice == K.TOOL_REQUIRED and not names:
+        return True
+    if kind == "partial":
+        return any(n[:len(v)] == v for n in allowed)
+    return v in allowed
+
+
+def _name_strings():
+    import itertools
+
+    # everything up to 5 bytes over the key's and value's bytes, and every string of the form
+    # <up to 2 bytes> "name" <up to 5 bytes> over the bytes that decide the scan
+    full = [b'"', b"n", b"a", b":", b"\\", b" ", b"x"]
+    for length in range(0, 6):
+        for combo in itertools.product(full, repeat=length):
+            yield b"".join(combo)
+    pre = [b'"', b"x", b" "]
+    post = [b'"', b":", b"\\", b" ", b"\t", b"l", b"x"]
+    heads = [b""] + [b"".join(c) for k in (1, 2) for c in itertools.product(pre, repeat=k)]
+    tails = [b"".join(c) for k in range(0, 6) for c in itertools.product(post, repeat=k)]
+    for h in heads:
+        for t in tails:
+            yield h + b'"name"' + t
+            yield b"{" + h + b'"name"' + t
+    # a second key after the first (the scan resumes after a non-colon; the first key's
+    # closing quote can open the second)
+    short = [t for t in tails if len(t) <= 3]
+    for h in heads[:4]:
+        for mid in (b"", b" ", b"x", b":", b'"', b"name"):
+            for t in short:
+                yield b"{" + h + b'"name"' + mid + b'"name"' + t
+
+
+def test_json_name_so_far_brute_force():
+    n = 0
+    for b in _name_strings():
+        assert K.json_name_so_far(b) == _name_so_far_independent(b), b
+        n += 1
+    assert n > 100000
+
+
+def test_tool_call_prefix_ok_brute_force():
+    names = [b"l", b"lx", b'l"']
+    n = 0
+    for b in _name_strings():
+        if not b.startswith(b"{"):
+            b = b"{" + b
+        for choice, named, nm in ((K.TOOL_REQUIRED, b"", names), (K.TOOL_REQUIRED, b"", []),
+                                  (K.TOOL_NAMED, b"lx", names), (K.TOOL_AUTO, b"", names)):
+            assert K.tool_call_prefix_ok(b, choice, named, nm) == _tool_ok_independent(b, choice, named, nm), (b, choice)
+            n += 1
+    assert n > 100000
