@@ -252,6 +252,17 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         for (int e = 0; e < EPV; e++) tk[q] |= (ev[q][e] >= egth && x[q][e] > -__builtin_inff()) ? 1u << e : 0u;
     }
 
+    // the candidates' positions in the row's list: a block scan and one global count per
+    // workgroup, issued now (its value is first needed at the end)
+    uint32_t gpos = 0, gtot = 0, gbase = 0;
+    if (gather) {
+        uint32_t nt = 0;
+#pragma unroll
+        for (int q = 0; q < QV; q++) nt += (uint32_t)__popc(tk[q]);
+        gpos = block_excl_scan<uint32_t>(nt, sm.wg, gtot);
+        if (gtot && tid == 0) gbase = glb_add(a.rowcnt + row, gtot);
+    }
+
     uint32_t qflags = QF_EXACT, qn = 0;  // this chunk's summary (for the first chunk's walk below)
     if (!trivial) {
         // the prediction: prefix sums of the terms (index order: vector, thread, element) from
@@ -292,10 +303,13 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         // classify and quantize: window bits (the interval straddles a binade boundary, a tie
         // of RN, or 2^23 units or more: the chain adds these exactly) and zero bits (e = 0:
         // nothing at any binade). The running sums below 2^-125 (the subnormals and the
-        // lowest normal binade) share one spacing, 2^-149: one binade. A certain element
-        // keeps (units << 8 | ue + 150).
-        uint32_t pk[QV][EPV];
-        uint32_t wm[QV], zm[QV];
+        // lowest normal binade) share one spacing, 2^-149: one binade. A certain element's
+        // units are recomputed from e where the runs are summed; each keeps its binade
+        // (ue + 150) in a byte of eb.
+        static_assert(QV * EPV <= 32, "one bit per element of a thread");
+        constexpr int EBW = (EPV + 3) / 4;  // words of packed binades per vector
+        uint32_t wmask = 0, zmask = 0;      // window and zero bits: bit q * EPV + e
+        uint32_t eb[QV][EBW];
 #pragma unroll
         for (int q = 0; q < QV; q++) {
             // the vector as a whole: the interval from before its first element to after its
@@ -330,17 +344,28 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                 const bool win = !zero & (((wq >> e) & 1u) | (fabsf(t - qf) == 0.5f) | !(t < 8388608.0f));
                 zq |= zero ? 1u << e : 0u;
                 wq = win ? wq | (1u << e) : wq & ~(1u << e);
-                pk[q][e] = (zero | win) ? 0u : ((uint32_t)qf << 8) | (elo_e[e] & 0xFFu);
             }
-            wm[q] = wq;
-            zm[q] = zq;
+#pragma unroll
+            for (int i = 0; i < EBW; i++) {
+                uint32_t wd = 0;
+#pragma unroll
+                for (int e = 4 * i; e < EPV && e < 4 * i + 4; e++) wd |= (elo_e[e] & 0xFFu) << (8 * (e - 4 * i));
+                eb[q][i] = wd;
+            }
+            wmask |= wq << (q * EPV);
+            zmask |= zq << (q * EPV);
         }
+        // an element's binade and units (certain elements)
+        auto elo_of = [&](int q, int e) { return (eb[q][e >> 2] >> (8 * (e & 3))) & 0xFFu; };
+        auto units_at = [&](int q, int e, uint32_t elo) {
+            return (uint32_t)__builtin_rintf(__builtin_ldexpf(ev[q][e], 150 - (int32_t)elo));
+        };
         BFI_TRACE(a, tb, 4);
         // window positions in index order
         uint32_t wpre[QV];
 #pragma unroll
         for (int q = 0; q < QV; q++) {
-            const uint32_t c = (uint32_t)__popc(wm[q]);
+            const uint32_t c = (uint32_t)__popc((wmask >> (q * EPV)) & em);
             const uint32_t incl = wave_scan_incl(c, 0u, [](uint32_t u, uint32_t v) { return u + v; });
             if (lane == WAVE - 1) sm.vc[q * NWAVE + w] = incl;
             wpre[q] = incl - c;
@@ -362,7 +387,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
 #pragma unroll
             for (int q = 0; q < QV; q++) {
                 const uint32_t id0 = c0 + (uint32_t)(q * BLOCK + tid) * EPV;
-                uint32_t m = wm[q];
+                uint32_t m = (wmask >> (q * EPV)) & em;
                 uint32_t pos = wpre[q];
                 while (m) {
                     const int i = __builtin_ctz(m);
@@ -387,15 +412,17 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             bool have = false;
 #pragma unroll
             for (int q = 0; q < QV; q++) {
-                if (wm[q] == 0u) {
-                    if (zm[q] == (1u << EPV) - 1u) continue;
+                const uint32_t wmq = (wmask >> (q * EPV)) & em, zmq = (zmask >> (q * EPV)) & em;
+                if (wmq == 0u) {
+                    if (zmq == em) continue;
                     uint32_t vq = 0, vh = 0, vl = 0xFFu;
 #pragma unroll
                     for (int e = 0; e < EPV; e++) {
-                        vq += pk[q][e] >> 8;
-                        const uint32_t b = pk[q][e] & 0xFFu;
-                        vh = max(vh, b);
-                        vl = ((zm[q] >> e) & 1u) ? vl : min(vl, b);
+                        const bool z = (zmq >> e) & 1u;
+                        const uint32_t b = elo_of(q, e);
+                        vq += z ? 0u : units_at(q, e, b);
+                        vh = z ? vh : max(vh, b);
+                        vl = z ? vl : min(vl, b);
                     }
                     const uint32_t k = wpre[q];
                     if (have && k != key) {
@@ -416,8 +443,8 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                 }
 #pragma unroll
                 for (int e = 0; e < EPV; e++) {
-                    if (((wm[q] | zm[q]) >> e) & 1u) continue;
-                    const uint32_t k = wpre[q] + (uint32_t)__popc(wm[q] & ((1u << e) - 1u));
+                    if (((wmq | zmq) >> e) & 1u) continue;
+                    const uint32_t k = wpre[q] + (uint32_t)__popc(wmq & ((1u << e) - 1u));
                     if (have && k != key) {
                         lds_add(&sm.rq[key], acc);
                         lds_max(&sm.rhi[key], khi);
@@ -429,8 +456,8 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                     }
                     have = true;
                     key = k;
-                    acc += pk[q][e] >> 8;
-                    const uint32_t b = pk[q][e] & 0xFFu;
+                    const uint32_t b = elo_of(q, e);
+                    acc += units_at(q, e, b);
                     klo = min(klo, b);
                     khi = max(khi, b);
                 }
@@ -460,23 +487,14 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             }
             __threadfence_block();
             __syncthreads();
-            // the items: the windows' exact values (the whole block, in window order) and the
-            // runs before them; then the tail run
+            // the items' runs (the window halves are written): the run before each window
+            // element, then the tail run
             for (uint32_t k = (uint32_t)tid; k <= nwin; k += BLOCK) {
                 const uint32_t q = sm.rq[k];
                 const uint32_t hi = sm.rhi[k];
                 const int32_t ue = hi ? (int32_t)hi - 150 : -(int32_t)UE_BIAS;  // empty: any binade
-                QItem it;
-                it.id = QI_NONE;
-                it.e = 0.0f;
-                if (k < nwin) {
-                    const uint2 wv = *reinterpret_cast<const uint2*>(&items[k]);
-                    it.id = wv.x;
-                    it.e = __uint_as_float(wv.y);
-                }
-                it.q = q;
-                it.ue = ue;
-                items[k] = it;
+                if (k < nwin) *reinterpret_cast<uint2*>(&items[k].q) = make_uint2(q, (uint32_t)ue);
+                else items[k] = QItem{QI_NONE, 0.0f, q, ue};
             }
             const uint32_t wb = __ballot(bad != 0u) ? 1u : 0u;
             if (lane == 0) sm.wb[w] = wb;
@@ -493,18 +511,12 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         if (a.trace && tid == 0) a.trace[tb + 6] = nwin;  // diagnostics: windows
     }
 
-    // the candidates of the kept set into the row's list, as (id, e): positions from a block
-    // scan, one global count per workgroup
+    // the candidates of the kept set into the row's list, as (id, e)
     if (gather) {
-        uint32_t nt = 0;
-#pragma unroll
-        for (int q = 0; q < QV; q++) nt += (uint32_t)__popc(tk[q]);
-        uint32_t tot;
-        uint32_t pos = block_excl_scan<uint32_t>(nt, sm.wg, tot);
-        if (tot) {
-            if (tid == 0) sm.gbase = glb_add(a.rowcnt + row, tot);
+        if (gtot) {
+            if (tid == 0) sm.gbase = gbase;
             __syncthreads();
-            pos += sm.gbase;
+            uint32_t pos = gpos + sm.gbase;
             uint64_t* list = a.spill + (int64_t)row * 4 * a.V;
 #pragma unroll
             for (int q = 0; q < QV; q++) {
