@@ -34,9 +34,11 @@ WORKLOAD_DESC = {
 
 
 def read_traffic(name):
-    """HBM bytes per launch of the streaming kernel from the committed rocprofv3 counter
-    summary (profiles/k_stream_<config>_traffic.txt, line 'traffic_bytes: N'), if present."""
-    p = os.path.join(ROOT, "profiles", f"k_stream_{name}_traffic.txt")
+    """HBM bytes per call (all three kernels) from the committed rocprofv3 counter summary
+    (profiles/sample_rows_<config>.txt or verify_<config>.txt, line 'traffic_bytes: N'), if
+    present."""
+    entry = "verify" if name == "C4" else "sample_rows"
+    p = os.path.join(ROOT, "profiles", f"{entry}_{name}.txt")
     try:
         for line in open(p):
             if line.startswith("traffic_bytes:"):
