@@ -41,6 +41,8 @@ struct __align__(16) RowSmem {
     uint32_t bcnt[NB];     // per bucket: element count
     uint32_t boff[NB];     // per bucket: first position in grp
     uint32_t bfill[NB];    // per bucket: fill counter, then scratch
+    uint32_t bsm[NB];      // per bucket: a walk's running sum before it, in units (recorded walks)
+    uint32_t bsx[NB];      //   and (rank << 10 | unit exponent + 512); 0: not recorded
     uint32_t coff[NCMAX + 1];  // the chain: first item of each chunk
     uint32_t cflag[NCMAX];     //   and its flags
     uint32_t wu[NWAVE];
@@ -753,6 +755,7 @@ struct ListInfo {
     int row;
     int small;          // n <= SORTCAP: the keys sorted in LDS, no buckets
     float* cum;         // small lists: LDS room for a walk's running sum after each element
+    uint32_t top, sh;   // bucketed lists: bucket of a key = top - (key >> 32 >> sh)
 };
 
 __device__ __forceinline__ float key_p(uint64_t key, bool idxmode) {
@@ -882,12 +885,15 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
     while ((hmax >> sh) - (hmin >> sh) >= (uint32_t)NB) sh++;
     const uint32_t top = hmax >> sh;
     L.nb = top - (hmin >> sh) + 1;
+    L.top = top;
+    L.sh = (uint32_t)sh;
     L.kmax = kmax;
     uint64_t* G = nv <= (uint32_t)LCAP ? sm.grp : a.spill + (int64_t)C.row * 4 * a.V + a.V;
     L.G = G;
     for (int b = tid; b < NB; b += BLOCK) {
         sm.bcnt[b] = 0u;
         sm.bfill[b] = 0u;
+        sm.bsx[b] = 0u;
     }
     __syncthreads();
     for (uint32_t j = tid; j < nv; j += BLOCK) {
@@ -1133,7 +1139,7 @@ __device__ __forceinline__ const uint64_t* sort_event_bucket(const ListInfo& L, 
 }
 
 __device__ __noinline__ WalkOut walk_big(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
-                                            uint64_t* gscratch) {
+                                            uint64_t* gscratch, bool rec, uint32_t from) {
     RowSmem& sm = g_sm;
     const int tid = threadIdx.x;
     uint32_t* const tq = sm.bfill;           // per thread: exclusive unit prefix of its keys
@@ -1145,9 +1151,19 @@ __device__ __noinline__ WalkOut walk_big(const ListInfo L, float th, uint32_t R,
     WalkOut o{0.0f, 0u, 0ull, 0};
     bool stopped = false;
     uint32_t b0 = 0;
+    if (from > 0u) {  // resume at a recorded bucket start
+        const uint32_t x = sm.bsx[from];
+        walk_set(w, state_value(sm.bsm[from], (int32_t)(x & 1023u) - 512), th);
+        w.r = x >> 10;
+        b0 = from;
+    }
     while (b0 < L.nb && !stopped) {
         // the round's buckets [b0, b1): whole buckets within one tile, at least one
         const uint32_t e0 = sm.boff[b0];
+        if (rec && tid == 0) {
+            sm.bsm[b0] = w.m;
+            sm.bsx[b0] = (w.r << 10) | (uint32_t)(w.ue + 512);
+        }
         uint32_t b1 = bucket_of(sm, L, b0, L.nb + 1, e0 + WTILE);
         if (b1 <= b0) b1 = b0 + 1;
         const uint32_t e1 = bucket_start(sm, L, b1);
@@ -1217,6 +1233,10 @@ __device__ __noinline__ WalkOut walk_big(const ListInfo L, float th, uint32_t R,
             w.r += sm.misc[MS_NV];
             __syncthreads();
         }
+        if (rec && tid == 0) {
+            sm.bsm[bs] = w.m;
+            sm.bsx[bs] = (w.r << 10) | (uint32_t)(w.ue + 512);
+        }
         // the bucket sorted, then walked element by element from that state (wave 0)
         const uint64_t* buf = sort_event_bucket(L, bs, gscratch, sm);
         const uint32_t n = sm.bcnt[bs];
@@ -1262,9 +1282,12 @@ __device__ __noinline__ WalkOut walk_big(const ListInfo L, float th, uint32_t R,
 // The walk: over a small (sorted) list or a bucketed list in LDS by wave 0, the result
 // broadcast through LDS to every thread; over a bucketed list in the spill area (more keys
 // than LDS holds) by the block (walk_big).
+// rec: a bucketed walk records the running state before the buckets it passes (bsm/bsx);
+// from: a bucketed walk starts at bucket `from` with the state recorded there (an earlier walk
+// over the same keys that excluded none, and an excluded key, if any, not before it).
 __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
-                                     uint64_t* gscratch, float* cum = nullptr) {
-    if (!L.small && L.n > (uint32_t)LCAP) return walk_big(L, th, R, excl, idxmode, gscratch);
+                                     uint64_t* gscratch, float* cum = nullptr, bool rec = false, uint32_t from = 0) {
+    if (!L.small && L.n > (uint32_t)LCAP) return walk_big(L, th, R, excl, idxmode, gscratch, rec, from);
     RowSmem& sm = g_sm;
     WalkOut o{0.0f, 0u, 0ull, 0};
     if (wave_id() == 0) {
@@ -1277,6 +1300,12 @@ __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, 
             stopped = walk_elems(w, j0 + (uint32_t)lane < L.n ? L.G[j0 + lane] : 0ull, th, R, excl, idxmode, o, cum);
         // a bucketed list in LDS: 64 buckets a step, each lane summing one bucket
         uint32_t b0 = 0;
+        if (!L.small && from > 0u) {
+            const uint32_t x = sm.bsx[from];
+            walk_set(w, state_value(sm.bsm[from], (int32_t)(x & 1023u) - 512), th);
+            w.r = x >> 10;
+            b0 = from;
+        }
         while (!L.small && b0 < L.nb && !stopped) {
             const uint32_t b = b0 + (uint32_t)lane;
             const uint32_t cnt = b < L.nb ? sm.bcnt[b] : 0u;
@@ -1296,6 +1325,16 @@ __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, 
             const uint32_t run = sat_add(w.m, Qi);
             const bool ev = c > 0 && (tie || run >= M_TOP || run >= w.tu || (uint64_t)w.r + Ci >= (uint64_t)R);
             const uint64_t bal = __ballot(ev);
+            if (rec) {  // the state before each bucket up to the first event's
+                const int s1 = bal ? __ffsll((unsigned long long)bal) - 1 : WAVE;
+                // (the shuffles run on every lane: a lane outside exec reads back as 0)
+                const uint32_t Qu = (uint32_t)__shfl_up((int)Qi, 1), Cu = (uint32_t)__shfl_up((int)Ci, 1);
+                const uint32_t Qx = lane ? Qu : 0u, Cx = lane ? Cu : 0u;
+                if (b < L.nb && lane <= s1) {
+                    sm.bsm[b] = sat_add(w.m, Qx);
+                    sm.bsx[b] = ((w.r + Cx) << 10) | (uint32_t)(w.ue + 512);
+                }
+            }
             if (!bal) {
                 w.m = lane63(run);
                 w.r += lane63(Ci);
@@ -1695,6 +1734,18 @@ __device__ __forceinline__ StreamArgs stream_args(const KArgs& a, const RowCtx& 
     return A;
 }
 
+// The bucket a bucketed walk toward threshold r can start at: the last bucket b <= bmax whose
+// recorded running state lies below r (0 when none, or for a small list). Every thread.
+__device__ __forceinline__ uint32_t walk_from(const ListInfo& L, float r, uint32_t bmax, RowSmem& sm) {
+    if (L.small) return 0u;
+    uint32_t best = 0u;
+    for (uint32_t b = (uint32_t)threadIdx.x; b <= bmax && b < L.nb; b += BLOCK) {
+        const uint32_t x = sm.bsx[b];
+        if (x && state_value(sm.bsm[b], (int32_t)(x & 1023u) - 512) < r) best = max(best, b);
+    }
+    return 0xFFFFFFFFu - block_min_u(0xFFFFFFFFu - best, sm.wu);
+}
+
 // The first index i < n with cum[i] >= r (n when none); cum is non-decreasing (a running sum
 // of non-negative terms). Wave 0 searches in two rounds of 64 probes; every thread gets it.
 __device__ __forceinline__ uint32_t first_ge(const float* cum, uint32_t n, float r, RowSmem& sm) {
@@ -1839,7 +1890,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
             uint32_t Lp = Lk;
             WalkOut o1{0.0f, 0u, 0ull, 0};
             if (C.pmode) {
-                o1 = walk(L, C.top_p, Lk, 0ull, 0, gscr, cum);
+                o1 = walk(L, C.top_p, Lk, 0ull, 0, gscr, cum, true);
                 if (cum) ncum = o1.how ? o1.rank + 1 : o1.rank;
                 if (o1.how == 1) Lp = o1.rank + 1;
                 else if (o1.how == 0 && !exhaustive) Lp = LINF;
@@ -1889,7 +1940,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
                 sum = cum[Lfin - 1];  // (not a judged row: klast unused)
                 klast = 0ull;
             } else {
-                const WalkOut o2 = walk(L, __builtin_inff(), Lfin, 0ull, 0, gscr, cum);
+                const WalkOut o2 = walk(L, __builtin_inff(), Lfin, 0ull, 0, gscr, cum, !C.pmode);
                 sum = o2.cum;
                 klast = o2.how == 2 ? o2.key : 0ull;
                 if (cum) ncum = o2.how ? o2.rank + 1 : o2.rank;
@@ -1906,7 +1957,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
                     const uint32_t i = first_ge(cum, nk, r, sm);
                     tok = i < nk ? key_id(L.G[i], false) : (Lfin <= L.n ? key_id(L.G[Lfin - 1], false) : 0u);
                 } else {
-                    const WalkOut o3 = walk(L, r, Lfin, 0ull, 0, gscr);
+                    const WalkOut o3 = walk(L, r, Lfin, 0ull, 0, gscr, nullptr, false, walk_from(L, r, L.nb, sm));
                     tok = o3.how ? key_id(o3.key, false) : 0u;
                 }
                 BFI_RTRACE(a, C, 8);
@@ -1935,9 +1986,18 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
             }
             const uint64_t ex = dk ? kd : 0ull;
             const uint32_t Lr = Lfin - (dk ? 1u : 0u);
-            const WalkOut o4 = walk(L, __builtin_inff(), Lr, ex, 0, gscr);
+            // the residual's walks: the recorded states before the draft's bucket hold for the
+            // residual too; the residual sum's walk records its own from there on, which the
+            // residual draw then starts from
+            const uint32_t bmax = dk && !L.small ? L.top - ((uint32_t)(kd >> 32) >> L.sh) : L.nb;
+            const uint32_t from4 = walk_from(L, __builtin_inff(), bmax, sm);
+            if (!L.small) {  // the full walk's records past the residual's start no longer hold
+                for (uint32_t b = from4 + 1u + (uint32_t)tid; b < L.nb; b += BLOCK) sm.bsx[b] = 0u;
+                __syncthreads();
+            }
+            const WalkOut o4 = walk(L, __builtin_inff(), Lr, ex, 0, gscr, nullptr, true, from4);
             const float r2 = C.u2 * fmaxf(o4.cum, 0.0f);
-            const WalkOut o5 = walk(L, r2, Lr, ex, 0, gscr);
+            const WalkOut o5 = walk(L, r2, Lr, ex, 0, gscr, nullptr, false, walk_from(L, r2, L.nb, sm));
             row_emit(a, sm, C, o5.how ? key_id(o5.key, false) : 0u, 0u);
             return;
         }
