@@ -43,6 +43,10 @@ struct __align__(16) RowSmem {
     uint32_t bfill[NB];    // per bucket: fill counter, then scratch
     uint32_t bsm[NB];      // per bucket: a walk's running sum before it, in units (recorded walks)
     uint32_t bsx[NB];      //   and (rank << 10 | unit exponent + 512); 0: not recorded
+    uint32_t bq[NB];       // per bucket: units its keys add at the predicted binade (bucket_units)
+    uint32_t bk[NB];       //   and that binade's unit exponent + 512 (0: none; bit 31: a tie of RN)
+    uint64_t pq_excl;      // the key bq leaves out
+    uint32_t pq_ok;        // bq/bk hold the current list's prediction
     uint32_t coff[NCMAX + 1];  // the chain: first item of each chunk
     uint32_t cflag[NCMAX];     //   and its flags
     uint32_t wu[NWAVE];
@@ -782,26 +786,35 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
     __syncthreads();
     uint32_t hmax = 0u, hmin = 0xFFFFFFFFu;
     uint64_t kmax = 0;
-    for (uint32_t j = tid; j < N; j += BLOCK) {
-        const uint64_t ent = src[j];
-        const uint32_t id = (uint32_t)(ent >> 32);
-        const float p = exact_p(__uint_as_float((uint32_t)ent), S);
-        const bool valid = p > 0.0f && p >= p_lo;
-        const uint64_t key = make_key(p, id, idxmode);
-        const uint64_t bal = __ballot(valid);
-        if (!bal) continue;
-        const int leader = __ffsll((unsigned long long)bal) - 1;
-        uint32_t base = 0;
-        if (lane_id() == leader) base = lds_add(&sm.misc[MS_NV], (uint32_t)__popcll(bal));
-        base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
-        if (valid) {
-            const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
-            if (pos < (uint32_t)LCAP) sm.list[pos] = key;
-            else ovf[pos] = key;
-            const uint32_t hi = (uint32_t)(key >> 32);
-            hmax = max(hmax, hi);
-            hmin = min(hmin, hi);
-            kmax = key > kmax ? key : kmax;
+    constexpr int BB = 8;  // entries loaded at once (global memory latency)
+    for (uint32_t j0 = tid; j0 < N; j0 += BB * BLOCK) {
+        uint64_t ent[BB];
+#pragma unroll
+        for (int i = 0; i < BB; i++) {
+            const uint32_t j = j0 + (uint32_t)(i * BLOCK);
+            ent[i] = j < N ? src[j] : 0ull;
+        }
+#pragma unroll
+        for (int i = 0; i < BB; i++) {
+            const uint32_t id = (uint32_t)(ent[i] >> 32);
+            const float p = exact_p(__uint_as_float((uint32_t)ent[i]), S);
+            const bool valid = j0 + (uint32_t)(i * BLOCK) < N && p > 0.0f && p >= p_lo;
+            const uint64_t key = make_key(p, id, idxmode);
+            const uint64_t bal = __ballot(valid);
+            if (!bal) continue;
+            const int leader = __ffsll((unsigned long long)bal) - 1;
+            uint32_t base = 0;
+            if (lane_id() == leader) base = lds_add(&sm.misc[MS_NV], (uint32_t)__popcll(bal));
+            base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
+            if (valid) {
+                const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
+                if (pos < (uint32_t)LCAP) sm.list[pos] = key;
+                else ovf[pos] = key;
+                const uint32_t hi = (uint32_t)(key >> 32);
+                hmax = max(hmax, hi);
+                hmin = min(hmin, hi);
+                kmax = key > kmax ? key : kmax;
+            }
         }
     }
     __threadfence_block();
@@ -895,10 +908,18 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
         sm.bfill[b] = 0u;
         sm.bsx[b] = 0u;
     }
+    if (tid == 0) sm.pq_ok = 0u;
     __syncthreads();
-    for (uint32_t j = tid; j < nv; j += BLOCK) {
-        const uint64_t key = j < (uint32_t)LCAP ? sm.list[j] : ovf[j];
-        lds_add(&sm.bcnt[top - ((uint32_t)(key >> 32) >> sh)], 1u);
+    for (uint32_t j0 = tid; j0 < nv; j0 += BB * BLOCK) {
+        uint64_t k[BB];
+#pragma unroll
+        for (int i = 0; i < BB; i++) {
+            const uint32_t j = j0 + (uint32_t)(i * BLOCK);
+            k[i] = j < nv ? (j < (uint32_t)LCAP ? sm.list[j] : ovf[j]) : 0ull;
+        }
+#pragma unroll
+        for (int i = 0; i < BB; i++)
+            if (k[i]) lds_add(&sm.bcnt[top - ((uint32_t)(k[i] >> 32) >> sh)], 1u);
     }
     __syncthreads();
     {
@@ -917,10 +938,22 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
             }
     }
     __syncthreads();
-    for (uint32_t j = tid; j < nv; j += BLOCK) {
-        const uint64_t key = j < (uint32_t)LCAP ? sm.list[j] : ovf[j];
-        const uint32_t b = top - ((uint32_t)(key >> 32) >> sh);
-        G[sm.boff[b] + lds_add(&sm.bfill[b], 1u)] = key;
+    for (uint32_t j0 = tid; j0 < nv; j0 += BB * BLOCK) {
+        uint64_t k[BB];
+#pragma unroll
+        for (int i = 0; i < BB; i++) {
+            const uint32_t j = j0 + (uint32_t)(i * BLOCK);
+            k[i] = j < nv ? (j < (uint32_t)LCAP ? sm.list[j] : ovf[j]) : 0ull;
+        }
+        uint32_t at[BB];
+#pragma unroll
+        for (int i = 0; i < BB; i++) {
+            const uint32_t b = top - ((uint32_t)(k[i] >> 32) >> sh);
+            at[i] = k[i] ? sm.boff[b] + lds_add(&sm.bfill[b], 1u) : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < BB; i++)
+            if (k[i]) G[at[i]] = k[i];
     }
     __threadfence_block();
     __syncthreads();
@@ -1138,6 +1171,108 @@ __device__ __forceinline__ const uint64_t* sort_event_bucket(const ListInfo& L, 
     return n2 <= LCAP ? sm.list : gscratch;  // (sort_bucket's buffer)
 }
 
+constexpr float PQ_EPS = 0x1p-13f;  // relative width of a bucket walk's predicted running sum
+
+// Per bucket of a bucketed list: the units its keys add at the binade a walk's running sum
+// lies in while it passes the bucket, as predicted from the real prefix of the bucket masses
+// widened by PQ_EPS both ways (bq; bk: that unit exponent + 512, 0 where the prediction
+// straddles a binade boundary, bit 31 where a key is a tie of RN there). The excluded key
+// adds nothing. A walk takes a bucket's bq in one step when its state lies in that binade;
+// a wrong prediction costs the bucket's serial sum, never the result. Every thread; each
+// sums a contiguous run of keys and adds to a bucket once per bucket it touches.
+__device__ __forceinline__ void bucket_units(const ListInfo& L, RowSmem& sm, uint64_t excl) {
+    constexpr int KB = 8;  // keys loaded at once (the list may sit in global memory)
+    const int tid = threadIdx.x;
+    float* const bm = reinterpret_cast<float*>(sm.bfill);  // per bucket: real mass
+    for (int b = tid; b < NB; b += BLOCK) {
+        bm[b] = 0.0f;
+        sm.bq[b] = 0u;
+    }
+    __syncthreads();
+    const uint32_t per = (L.n + BLOCK - 1u) / BLOCK;
+    const uint32_t j0 = min((uint32_t)tid * per, L.n), j1 = min(j0 + per, L.n);
+    {
+        uint32_t cb = 0xFFFFFFFFu;
+        float acc = 0.0f;
+        for (uint32_t jb = j0; jb < j1; jb += KB) {
+            uint64_t k[KB];
+#pragma unroll
+            for (int i = 0; i < KB; i++) k[i] = jb + (uint32_t)i < j1 ? L.G[jb + i] : 0ull;
+#pragma unroll
+            for (int i = 0; i < KB; i++) {
+                if (!k[i]) continue;
+                const uint32_t b = L.top - ((uint32_t)(k[i] >> 32) >> L.sh);
+                if (b != cb) {
+                    if (cb != 0xFFFFFFFFu) atomicAdd(&bm[cb], acc);
+                    cb = b;
+                    acc = 0.0f;
+                }
+                acc += k[i] == excl ? 0.0f : key_p(k[i], false);
+            }
+        }
+        if (cb != 0xFFFFFFFFu) atomicAdd(&bm[cb], acc);
+    }
+    __syncthreads();
+    {
+        static_assert(NB == 2 * BLOCK, "two buckets a thread");
+        const uint32_t b0 = 2u * (uint32_t)tid;
+        const float m0 = bm[b0], m1 = bm[b0 + 1u];
+        float tot;
+        const float P0 = block_excl_scan<float>(m0 + m1, sm.wf, tot);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t b = b0 + (uint32_t)i;
+            const float P = i ? P0 + m0 : P0, m = i ? m1 : m0;
+            uint32_t k = 0u;
+            if (b < L.nb && m > 0.0f && P > 0.0f) {
+                const float lo = P * (1.0f - PQ_EPS), hi = (P + m) * (1.0f + PQ_EPS);
+                const uint32_t elo = max(__float_as_uint(lo) >> 23, 1u), ehi = max(__float_as_uint(hi) >> 23, 1u);
+                if (elo == ehi) k = elo - 150u + 512u;
+            }
+            sm.bk[b] = k;
+        }
+    }
+    __syncthreads();
+    {
+        uint32_t cb = 0xFFFFFFFFu, q = 0u, kb = 0u;
+        bool tie = false;
+        for (uint32_t jb = j0; jb < j1; jb += KB) {
+            uint64_t k[KB];
+#pragma unroll
+            for (int i = 0; i < KB; i++) k[i] = jb + (uint32_t)i < j1 ? L.G[jb + i] : 0ull;
+#pragma unroll
+            for (int i = 0; i < KB; i++) {
+                if (!k[i]) continue;
+                const uint32_t b = L.top - ((uint32_t)(k[i] >> 32) >> L.sh);
+                if (b != cb) {
+                    if (kb) {
+                        atomicAdd(&sm.bq[cb], min(q, M_TOP));
+                        if (tie) atomicOr(&sm.bk[cb], 0x80000000u);
+                    }
+                    cb = b;
+                    q = 0u;
+                    tie = false;
+                    kb = sm.bk[b] & 0x3FFu;
+                }
+                if (kb && k[i] != excl) {
+                    const float t = units_of(key_p(k[i], false), (int32_t)kb - 512);
+                    q = sat_add(q, quant_units(t));
+                    tie = tie || quant_tie(t);
+                }
+            }
+        }
+        if (kb) {
+            atomicAdd(&sm.bq[cb], min(q, M_TOP));
+            if (tie) atomicOr(&sm.bk[cb], 0x80000000u);
+        }
+    }
+    if (tid == 0) {
+        sm.pq_excl = excl;
+        sm.pq_ok = 1u;
+    }
+    __syncthreads();
+}
+
 __device__ __noinline__ WalkOut walk_big(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
                                             uint64_t* gscratch, bool rec, uint32_t from) {
     RowSmem& sm = g_sm;
@@ -1281,87 +1416,123 @@ __device__ __noinline__ WalkOut walk_big(const ListInfo L, float th, uint32_t R,
 
 // The walk: over a small (sorted) list or a bucketed list in LDS by wave 0, the result
 // broadcast through LDS to every thread; over a bucketed list in the spill area (more keys
-// than LDS holds) by the block (walk_big).
+// than LDS holds) by the block (walk_big). In LDS, wave 0 sums 64 buckets a step and walks
+// the event buckets of up to 64 keys itself; a larger event bucket is sorted by the block.
 // rec: a bucketed walk records the running state before the buckets it passes (bsm/bsx);
 // from: a bucketed walk starts at bucket `from` with the state recorded there (an earlier walk
 // over the same keys that excluded none, and an excluded key, if any, not before it).
 __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, uint64_t excl, int32_t idxmode,
                                      uint64_t* gscratch, float* cum = nullptr, bool rec = false, uint32_t from = 0) {
-    if (!L.small && L.n > (uint32_t)LCAP) return walk_big(L, th, R, excl, idxmode, gscratch, rec, from);
     RowSmem& sm = g_sm;
+    // buckets whose predicted units hold at the walk's binade take them whole; the others are
+    // walked element by element (without a prediction: summed one key at a time, by the block
+    // for a list in the spill area)
+    const bool pq = !idxmode && !L.small && sm.pq_ok && sm.pq_excl == excl;
+    if (!L.small && L.n > (uint32_t)LCAP && !pq) return walk_big(L, th, R, excl, idxmode, gscratch, rec, from);
     WalkOut o{0.0f, 0u, 0ull, 0};
-    if (wave_id() == 0) {
-        const int lane = lane_id();
-        WalkState w;
-        walk_set(w, 0.0f, th);
-        w.r = 0;
-        bool stopped = false;
-        for (uint32_t j0 = 0; L.small && j0 < L.n && !stopped; j0 += WAVE)
-            stopped = walk_elems(w, j0 + (uint32_t)lane < L.n ? L.G[j0 + lane] : 0ull, th, R, excl, idxmode, o, cum);
-        // a bucketed list in LDS: 64 buckets a step, each lane summing one bucket
+    const int lane = lane_id();
+    // (the walk's state lives in wave 0; the other waves only help sort large event buckets)
+    WalkState w;
+    walk_set(w, 0.0f, th);
+    w.r = 0;
+    bool stopped = false;
+    if (L.small) {
+        if (wave_id() == 0)
+            for (uint32_t j0 = 0; j0 < L.n && !stopped; j0 += WAVE)
+                stopped = walk_elems(w, j0 + (uint32_t)lane < L.n ? L.G[j0 + lane] : 0ull, th, R, excl, idxmode, o, cum);
+    } else {
         uint32_t b0 = 0;
-        if (!L.small && from > 0u) {
+        if (from > 0u) {
             const uint32_t x = sm.bsx[from];
             walk_set(w, state_value(sm.bsm[from], (int32_t)(x & 1023u) - 512), th);
             w.r = x >> 10;
             b0 = from;
         }
-        while (!L.small && b0 < L.nb && !stopped) {
-            const uint32_t b = b0 + (uint32_t)lane;
-            const uint32_t cnt = b < L.nb ? sm.bcnt[b] : 0u;
-            const uint32_t off = b < L.nb ? sm.boff[b] : 0u;
-            uint32_t Q = 0, c = 0;
-            bool tie = false;
-            for (uint32_t j = 0; j < cnt; j++) {
-                const uint64_t key = L.G[off + j];
-                if (key == excl) continue;
-                const float t = units_of(key_p(key, idxmode), w.ue);
-                Q = sat_add(Q, quant_units(t));
-                tie = tie || quant_tie(t);
-                c++;
-            }
-            const uint32_t Qi = wave_scan_sat(Q);
-            const uint32_t Ci = wave_scan_incl(c, 0u, [](uint32_t x, uint32_t y) { return x + y; });
-            const uint32_t run = sat_add(w.m, Qi);
-            const bool ev = c > 0 && (tie || run >= M_TOP || run >= w.tu || (uint64_t)w.r + Ci >= (uint64_t)R);
-            const uint64_t bal = __ballot(ev);
-            if (rec) {  // the state before each bucket up to the first event's
-                const int s1 = bal ? __ffsll((unsigned long long)bal) - 1 : WAVE;
-                // (the shuffles run on every lane: a lane outside exec reads back as 0)
-                const uint32_t Qu = (uint32_t)__shfl_up((int)Qi, 1), Cu = (uint32_t)__shfl_up((int)Ci, 1);
-                const uint32_t Qx = lane ? Qu : 0u, Cx = lane ? Cu : 0u;
-                if (b < L.nb && lane <= s1) {
-                    sm.bsm[b] = sat_add(w.m, Qx);
-                    sm.bsx[b] = ((w.r + Cx) << 10) | (uint32_t)(w.ue + 512);
+        const uint32_t bex = excl ? L.top - ((uint32_t)(excl >> 32) >> L.sh) : 0xFFFFFFFFu;
+        for (;;) {
+            uint32_t big = L.nb;  // an event bucket of more than 64 keys (nb: the walk is over)
+            if (wave_id() == 0) {
+                while (b0 < L.nb && !stopped) {
+                    const uint32_t b = b0 + (uint32_t)lane;
+                    const uint32_t cnt = b < L.nb ? sm.bcnt[b] : 0u;
+                    const uint32_t off = b < L.nb ? sm.boff[b] : 0u;
+                    const uint32_t kb = pq && b < L.nb ? sm.bk[b] : 0u;
+                    uint32_t Q = 0, c = 0;
+                    bool tie = false, force = false;
+                    if (pq) {
+                        if (kb == (uint32_t)(w.ue + 512) && b != bex) {
+                            Q = sm.bq[b];
+                            c = cnt;
+                        } else {
+                            force = cnt > 0u;
+                        }
+                    } else {
+                        for (uint32_t j = 0; j < cnt; j++) {
+                            const uint64_t key = L.G[off + j];
+                            if (key == excl) continue;
+                            const float t = units_of(key_p(key, idxmode), w.ue);
+                            Q = sat_add(Q, quant_units(t));
+                            tie = tie || quant_tie(t);
+                            c++;
+                        }
+                    }
+                    const uint32_t Qi = wave_scan_sat(Q);
+                    const uint32_t Ci = wave_scan_incl(c, 0u, [](uint32_t x, uint32_t y) { return x + y; });
+                    const uint32_t run = sat_add(w.m, Qi);
+                    const bool ev =
+                        force || (c > 0 && (tie || run >= M_TOP || run >= w.tu || (uint64_t)w.r + Ci >= (uint64_t)R));
+                    const uint64_t bal = __ballot(ev);
+                    if (rec) {  // the state before each bucket up to the first event's
+                        const int s1 = bal ? __ffsll((unsigned long long)bal) - 1 : WAVE;
+                        // (the shuffles run on every lane: a lane outside exec reads back as 0)
+                        const uint32_t Qu = (uint32_t)__shfl_up((int)Qi, 1), Cu = (uint32_t)__shfl_up((int)Ci, 1);
+                        const uint32_t Qx = lane ? Qu : 0u, Cx = lane ? Cu : 0u;
+                        if (b < L.nb && lane <= s1) {
+                            sm.bsm[b] = sat_add(w.m, Qx);
+                            sm.bsx[b] = ((w.r + Cx) << 10) | (uint32_t)(w.ue + 512);
+                        }
+                    }
+                    if (!bal) {
+                        w.m = lane63(run);
+                        w.r += lane63(Ci);
+                        b0 += WAVE;
+                        continue;
+                    }
+                    const int s = __ffsll((unsigned long long)bal) - 1;
+                    if (s > 0) {
+                        w.m = (uint32_t)__builtin_amdgcn_readlane((int)run, s - 1);
+                        w.r += (uint32_t)__builtin_amdgcn_readlane((int)Ci, s - 1);
+                    }
+                    // the bucket of the event, sorted and walked element by element
+                    const uint32_t bs = b0 + (uint32_t)s;
+                    const uint32_t n = sm.bcnt[bs], o0 = sm.boff[bs];
+                    if (n > (uint32_t)WAVE) {
+                        big = bs;
+                        break;
+                    }
+                    uint64_t key = (uint32_t)lane < n ? L.G[o0 + lane] : 0ull;
+                    key = wave_sort_desc(key);
+                    stopped = walk_elems(w, key, th, R, excl, idxmode, o, nullptr);
+                    b0 = bs + 1;
                 }
+                if (lane == 0) sm.misc[MS_CNEXT] = big;
             }
-            if (!bal) {
-                w.m = lane63(run);
-                w.r += lane63(Ci);
-                b0 += WAVE;
-                continue;
+            __syncthreads();
+            big = sm.misc[MS_CNEXT];
+            __syncthreads();
+            if (big >= L.nb) break;
+            const uint64_t* buf = sort_event_bucket(L, big, gscratch, sm);
+            if (wave_id() == 0) {
+                const uint32_t n = sm.bcnt[big];
+                for (uint32_t j0 = 0; j0 < n && !stopped; j0 += WAVE)
+                    stopped = walk_elems(w, j0 + (uint32_t)lane < n ? buf[j0 + lane] : 0ull, th, R, excl, idxmode, o,
+                                         nullptr);
+                b0 = big + 1;
             }
-            const int s = __ffsll((unsigned long long)bal) - 1;
-            if (s > 0) {
-                w.m = (uint32_t)__builtin_amdgcn_readlane((int)run, s - 1);
-                w.r += (uint32_t)__builtin_amdgcn_readlane((int)Ci, s - 1);
-            }
-            // the bucket of the event, sorted and walked element by element
-            const uint32_t bs = b0 + (uint32_t)s;
-            const uint32_t n = sm.bcnt[bs], o0 = sm.boff[bs];
-            if (n <= (uint32_t)WAVE) {
-                uint64_t key = (uint32_t)lane < n ? L.G[o0 + lane] : 0ull;
-                key = wave_sort_desc(key);
-                stopped = walk_elems(w, key, th, R, excl, idxmode, o, nullptr);
-            } else {
-                int n2 = WAVE;
-                while ((uint32_t)n2 < n) n2 <<= 1;
-                const uint64_t* buf = sort_bucket(gscratch, L.G + o0, n, n2);
-                for (int j0 = 0; j0 < (int)n && !stopped; j0 += WAVE)
-                    stopped = walk_elems(w, buf[j0 + lane], th, R, excl, idxmode, o, nullptr);
-            }
-            b0 = bs + 1;
+            __syncthreads();  // (the sorted copy is read before the next sort overwrites it)
         }
+    }
+    if (wave_id() == 0) {
         if (!stopped) {
             o.cum = state_value(w.m, w.ue);
             o.rank = w.r;
@@ -1882,6 +2053,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
         for (int attempt = 0; attempt < 2; attempt++) {
             const float p_lo = exhaustive ? 0.0f : (float)(exp2((double)th) / (double)S * (1.0 + 0x1p-20));
             const ListInfo L = build_list(a, sm, C, N, M, S, p_lo, false);
+            if (!L.small) bucket_units(L, sm, 0ull);
             BFI_RTRACE(a, C, 5);
             // top-p (sample.rs:397-409); a sampled row's walks over a small list keep the
             // running sum after each element, from which the kept sum and the draw are read
@@ -1995,6 +2167,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
                 for (uint32_t b = from4 + 1u + (uint32_t)tid; b < L.nb; b += BLOCK) sm.bsx[b] = 0u;
                 __syncthreads();
             }
+            if (ex && !L.small) bucket_units(L, sm, ex);
             const WalkOut o4 = walk(L, __builtin_inff(), Lr, ex, 0, gscr, nullptr, true, from4);
             const float r2 = C.u2 * fmaxf(o4.cum, 0.0f);
             const WalkOut o5 = walk(L, r2, Lr, ex, 0, gscr, nullptr, false, walk_from(L, r2, L.nb, sm));
