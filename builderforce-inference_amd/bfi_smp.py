@@ -85,6 +85,24 @@ def lib():
         L.bfi_mask_error.restype = ctypes.c_char_p
         L.bfi_mask_set_vocab.argtypes = [P, P, P, I64]
         L.bfi_mask_build.argtypes = [P, P, I64, ctypes.POINTER(Constraint), P, ctypes.POINTER(ctypes.c_int32), P]
+        # prefix cache (include/bfi_prefix.h)
+        U64 = ctypes.c_uint64
+        L.bfi_pc_create.argtypes = [I32, U64, ctypes.POINTER(P)]
+        L.bfi_pc_destroy.argtypes = [P]
+        L.bfi_pc_destroy.restype = None
+        L.bfi_pc_last_error.argtypes = [P]
+        L.bfi_pc_last_error.restype = ctypes.c_char_p
+        L.bfi_pc_lookup.argtypes = [P, P, U64, ctypes.POINTER(PCHit), ctypes.POINTER(I32)]
+        L.bfi_pc_restore.argtypes = [P, ctypes.POINTER(PCHit), ctypes.POINTER(PCState), ctypes.POINTER(U64),
+                                     ctypes.POINTER(I32), ctypes.POINTER(I32), P]
+        L.bfi_pc_insert.argtypes = [P, P, U64, ctypes.POINTER(PCState), P]
+        for f in ("bfi_pc_used_bytes", "bfi_pc_len", "bfi_pc_forwarded"):
+            getattr(L, f).argtypes = [P]
+            getattr(L, f).restype = U64
+        L.bfi_pc_note_forward.argtypes = [P, U64]
+        L.bfi_pc_note_forward.restype = None
+        L.bfi_pc_clear.argtypes = [P]
+        L.bfi_pc_clear.restype = None
         _lib = L
     return _lib
 
@@ -105,6 +123,23 @@ class Constraint(ctypes.Structure):
         ("grammar", ctypes.c_void_p),
         ("grammar_len", ctypes.c_int64),
     ]
+
+
+class PCTensor(ctypes.Structure):
+    """bfi_pc_tensor (include/bfi_prefix.h)."""
+    _fields_ = [("data", ctypes.c_void_p), ("row_bytes", ctypes.c_uint64), ("rows", ctypes.c_uint64)]
+
+
+class PCState(ctypes.Structure):
+    """bfi_pc_state (include/bfi_prefix.h)."""
+    _fields_ = [("n", ctypes.c_uint64), ("kv", ctypes.c_void_p), ("n_kv", ctypes.c_uint64),
+                ("rec", ctypes.c_void_p), ("n_rec", ctypes.c_uint64), ("logits", ctypes.c_void_p),
+                ("n_logits", ctypes.c_uint64)]
+
+
+class PCHit(ctypes.Structure):
+    """bfi_pc_hit (include/bfi_prefix.h)."""
+    _fields_ = [("id", ctypes.c_uint64), ("matched", ctypes.c_uint64), ("restore", ctypes.c_uint64)]
 
 
 def params_array(rows) -> np.ndarray:
@@ -389,3 +424,112 @@ class MaskProducer:
             self.close()
         except Exception:
             pass
+
+
+# ---- prefix cache (include/bfi_prefix.h; engine/prefix.rs) ---------------------------------
+
+
+def _addr(a):
+    """Address of a numpy array (host cache) or a torch tensor (device cache)."""
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        assert a.flags.c_contiguous
+        return a.ctypes.data
+    assert a.is_contiguous()
+    return a.data_ptr()
+
+
+def _nbytes(a):
+    return a.nbytes if isinstance(a, np.ndarray) else a.numel() * a.element_size()
+
+
+class PrefixCache:
+    """PrefixCache (engine/prefix.rs:114-347) over the C ABI. device=-1 keeps entries in host
+    memory (numpy arrays in and out), device>=0 in that GPU's memory (torch tensors on it).
+
+    A state is (n, kv, rec, logits): kv a list of tensors whose first dimension is the
+    position (their first n rows are kept), or whole tensors (indices in `whole`); rec a list
+    of recurrent tensors or None per layer; logits a float32 vector."""
+
+    def __init__(self, budget_bytes: int, device: int = -1):
+        self._L = lib()
+        self._pc = ctypes.c_void_p()
+        rc = self._L.bfi_pc_create(device, budget_bytes, ctypes.byref(self._pc))
+        if rc != 0:
+            raise SamplerError(f"bfi_pc_create({device}) failed: {rc}")
+        self.device = device
+
+    def close(self):
+        if self._pc:
+            self._L.bfi_pc_destroy(self._pc)
+            self._pc = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise SamplerError(f"{what}: {self._L.bfi_pc_last_error(self._pc).decode()} (status {rc})")
+
+    @staticmethod
+    def _state(n, kv, rec, logits, whole=()):
+        ts = (PCTensor * max(len(kv), 1))()
+        for i, t in enumerate(kv):
+            if i in whole:
+                ts[i] = PCTensor(_addr(t), 0, _nbytes(t))
+            else:
+                rows = t.shape[0]
+                ts[i] = PCTensor(_addr(t), _nbytes(t) // rows if rows else 0, rows)
+        rs = (PCTensor * max(len(rec), 1))()
+        for i, t in enumerate(rec):
+            rs[i] = PCTensor(None, 0, 0) if t is None else PCTensor(_addr(t), 0, _nbytes(t))
+        nl = 0 if logits is None else (logits.size if isinstance(logits, np.ndarray) else logits.numel())
+        st = PCState(n, ctypes.cast(ts, ctypes.c_void_p), len(kv), ctypes.cast(rs, ctypes.c_void_p), len(rec),
+                     _addr(logits), nl)
+        return st, (ts, rs)
+
+    def lookup(self, ids):
+        """prefix.rs:168-214: (id, matched, restore) or None."""
+        a = np.ascontiguousarray(np.asarray(ids, np.uint32))
+        hit, found = PCHit(), ctypes.c_int32(0)
+        self._check(self._L.bfi_pc_lookup(self._pc, _np_ptr(a), a.size, ctypes.byref(hit), ctypes.byref(found)),
+                    "bfi_pc_lookup")
+        return (hit.id, hit.matched, hit.restore) if found.value else None
+
+    def prepare(self, n, kv, rec, logits, whole=()):
+        """The C description of a state, built once for calls that reuse the same tensors."""
+        return self._state(n, kv, rec, logits, whole)
+
+    def restore(self, hit, kv=None, rec=None, logits=None, whole=(), stream=None, prepared=None):
+        """prefix.rs:217-230 into the given full-capacity tensors: (n, logits_restored) or None."""
+        st, keep = prepared if prepared is not None else self._state(0, kv, rec, logits, whole)
+        h = PCHit(*hit)
+        n, lr, found = ctypes.c_uint64(0), ctypes.c_int32(0), ctypes.c_int32(0)
+        self._check(self._L.bfi_pc_restore(self._pc, ctypes.byref(h), ctypes.byref(st), ctypes.byref(n),
+                                           ctypes.byref(lr), ctypes.byref(found), stream), "bfi_pc_restore")
+        return (n.value, bool(lr.value)) if found.value else None
+
+    def insert(self, tokens, n=None, kv=None, rec=None, logits=None, whole=(), stream=None, prepared=None):
+        """prefix.rs:233-260 (insert_copy / insert_owned)."""
+        a = np.ascontiguousarray(np.asarray(tokens, np.uint32))
+        st, keep = prepared if prepared is not None else self._state(n, kv, rec, logits, whole)
+        self._check(self._L.bfi_pc_insert(self._pc, _np_ptr(a), a.size, ctypes.byref(st), stream), "bfi_pc_insert")
+
+    def used_bytes(self):
+        return self._L.bfi_pc_used_bytes(self._pc)
+
+    def __len__(self):
+        return self._L.bfi_pc_len(self._pc)
+
+    def note_forward(self, n):
+        self._L.bfi_pc_note_forward(self._pc, n)
+
+    def forwarded(self):
+        return self._L.bfi_pc_forwarded(self._pc)
+
+    def clear(self):
+        self._L.bfi_pc_clear(self._pc)

@@ -15,7 +15,7 @@ import oracle as O
 import workloads
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("bfi_sampler.h", "bfi_mask.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("bfi_sampler.h", "bfi_mask.h", "bfi_prefix.h")]
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
