@@ -152,6 +152,71 @@ def bench_mask(args):
     mp.close()
 
 
+def bench_head(args):
+    """The device output head (bfi_smp_head: rms_norm + lm_head with the reference's
+    rounding) and the fused head + sample step (bfi_smp_head_sample_rows) on a
+    Qwen3-0.6B-shaped head: 64 rows (C2's batch), n_embd 1024, n_vocab 151936, f32 weights
+    (622 MB), C2's per-row parameters and histories. Timed with events on the stream over
+    `--steps` calls after `--warmup`. The CPU baseline is the oracle's head (one thread) on
+    one row."""
+    import numpy as np
+    import torch
+
+    import bfi_smp
+    import oracle as O
+    import workloads
+
+    T, d, V = 64, 1024, 151936
+    rng = np.random.default_rng(args.seed)
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy((rng.standard_normal((T, d)) * 3).astype(np.float32)).to(dev)
+    nw = torch.from_numpy(rng.standard_normal(d).astype(np.float32)).to(dev)
+    w = torch.from_numpy((rng.standard_normal((V, d)) * (8 / np.sqrt(d))).astype(np.float32)).to(dev)
+    cfg = workloads.config("C2", seed=args.seed)
+    dd = workloads.to_device(cfg, dev)
+    smp = bfi_smp.Sampler(0)
+    logits = torch.empty((T, V), dtype=torch.float32, device=dev)
+    out = torch.zeros(T, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream()
+
+    def timed(fn, steps, warm):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(steps):
+            fn()
+        e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps * 1e-3
+
+    steps, warm = max(5, min(args.steps, 50)), max(2, min(args.warmup, 5))
+    t_head = timed(lambda: smp.head(x, nw, 1e-6, w, out=logits), steps, warm)
+    t_fused = timed(lambda: smp.head_sample_rows(x, nw, 1e-6, w, dd["params"], dd["u"], out, dd["hist"],
+                                                 dd["hist_off"]), steps, warm)
+    flops = 2.0 * T * V * d
+    achieved = flops / t_head / 1e12
+    xs = x[:1].cpu().numpy()
+    ws = w.cpu().numpy()
+    t0 = time.perf_counter()
+    O.matmul_f32(ws, O.rms_norm(xs, nw.cpu().numpy(), 1e-6))
+    t_cpu = time.perf_counter() - t0
+    line = {"metric": "device head + sample rows/sec (Qwen3-0.6B-shaped head, B=64)",
+            "value": round(T / t_fused, 1), "unit": "rows/s", "n_gpus": 1, "higher_is_better": True,
+            "head_ms": round(t_head * 1e3, 3), "head_sample_ms": round(t_fused * 1e3, 3),
+            "readback_bytes_per_row": 4, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "F2 head + sample", "rows": T, "n_embd": d, "n_vocab": V},
+            "roofline": {"bound": "valu", "achieved": round(achieved, 2), "peak": 157.3, "unit": "TFLOP/s",
+                         "frac": round(achieved / 157.3, 4), "traffic": V * d * 4 + T * (d + V) * 4,
+                         "note": "products and sums separately rounded (the reference's order): one "
+                                 "unpacked multiply and one add a term, no MFMA"},
+            "cpu_baseline": {"value": round(1.0 / t_cpu, 3), "unit": "rows/s", "cores": 1, "kind": "port",
+                             "sample": "the oracle's head on one row"}}
+    print(json.dumps(line), flush=True)
+    smp.close()
+
+
 def bench_prefix(args):
     """The prefix cache (include/bfi_prefix.h, engine/prefix.rs) on a Qwen3-0.6B-shaped state:
     28 layers x (K, V) of [4096 positions, 8 heads x 128] f32 rows (4 KiB a row), 2048 positions
@@ -255,6 +320,9 @@ def main():
     ap.add_argument("--mask", action="store_true",
                     help="measure the allow-mask producer (include/bfi_mask.h) instead: a named "
                          "tool-call constraint over a synthetic 151,936-piece vocabulary")
+    ap.add_argument("--head", action="store_true",
+                    help="measure the device output head (rms_norm + lm_head, the reference's rounding) and "
+                         "the fused head + sample step on a Qwen3-0.6B-shaped head instead")
     ap.add_argument("--prefix", action="store_true",
                     help="measure the prefix cache (include/bfi_prefix.h) instead: insert, restore and "
                          "lookup of a Qwen3-0.6B-shaped state in device memory")
@@ -285,6 +353,9 @@ def main():
         return
     if args.prefix:
         bench_prefix(args)
+        return
+    if args.head:
+        bench_head(args)
         return
 
     cfg = workloads.config(args.config, seed=args.seed)

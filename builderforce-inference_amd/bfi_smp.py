@@ -65,6 +65,9 @@ def lib():
         L.bfi_smp_target_rows.argtypes = [P, P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P, P, P, P, P, I64, P, P]
         L.bfi_smp_verify.argtypes = [P, P, I32, I64, I64, I64, I64, P, P, P, P, P, P, I64, P, P, P, P, P]
         L.bfi_smp_sample_host.argtypes = [P, P, I64, P, I64, P, P, ctypes.c_float, P]
+        L.bfi_smp_head.argtypes = [P, P, P, I32, ctypes.c_float, P, I64, I64, I64, P, P]
+        L.bfi_smp_head_sample_rows.argtypes = [P, P, P, I32, ctypes.c_float, P, I64, I64, I64, P, P, P, P, I64, P, P,
+                                               P]
         L.bfi_rng_next_u64.argtypes = [P]
         L.bfi_rng_next_u64.restype = ctypes.c_uint64
         L.bfi_rng_f32.argtypes = [P]
@@ -282,6 +285,34 @@ class Sampler:
                                          _dptr(hist), _dptr(hist_off), _dptr(mask), ms, _dptr(u), _dptr(out),
                                          self._stream(stream))
         self._check(rc, "bfi_smp_sample_rows")
+        return out
+
+    def head(self, x, norm_w, eps, w, out=None, norm_per_row=False, stream=None):
+        """The output head on the device (qwen3.rs:258-265): rms_norm then lm_head over f32
+        weights, bit-identical to the reference's CPU backend. x: cuda f32 [T, d]; norm_w:
+        [d] (or [T, d]); w: [V, d]; returns the [T, V] f32 logits."""
+        import torch
+
+        T, d = x.shape
+        V = w.shape[0]
+        if out is None:
+            out = torch.empty((T, V), dtype=torch.float32, device=x.device)
+        rc = self._L.bfi_smp_head(self._ctx, _dptr(x), _dptr(norm_w), 1 if norm_per_row else 0, ctypes.c_float(eps),
+                                  _dptr(w), T, d, V, _dptr(out), self._stream(stream))
+        self._check(rc, "bfi_smp_head")
+        return out
+
+    def head_sample_rows(self, x, norm_w, eps, w, params, u, out, hist=None, hist_off=None, mask=None,
+                         norm_per_row=False, stream=None):
+        """The fused device step: head, then sample_rows over its logits; out: cuda int32 [T]."""
+        T, d = x.shape
+        V = w.shape[0]
+        ms = 0 if mask is None else mask.stride(0)
+        rc = self._L.bfi_smp_head_sample_rows(self._ctx, _dptr(x), _dptr(norm_w), 1 if norm_per_row else 0,
+                                              ctypes.c_float(eps), _dptr(w), T, d, V, _dptr(params), _dptr(hist),
+                                              _dptr(hist_off), _dptr(mask), ms, _dptr(u), _dptr(out),
+                                              self._stream(stream))
+        self._check(rc, "bfi_smp_head_sample_rows")
         return out
 
     def sample_rows_noalloc(self, logits, params, u, out, hist=None, hist_off=None, mask=None, stream=None):

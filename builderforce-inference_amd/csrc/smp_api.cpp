@@ -57,6 +57,8 @@ namespace bfi {
 hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 hipError_t launch_quant(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 hipError_t launch_row(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+hipError_t launch_head(const float* x, const float* norm_w, int norm_per_row, float eps, const float* W, int64_t n_tok,
+                       int64_t d, int64_t n_out, int vec, float* xn, float* out, hipStream_t stream);
 }
 
 struct bfi_smp_ctx {
@@ -70,6 +72,9 @@ struct bfi_smp_ctx {
     // staging for bfi_smp_sample_host
     char* stage = nullptr;
     size_t stage_size = 0;
+    // the output head's workspace: normalized rows, then (head_sample_rows) the logits
+    char* head = nullptr;
+    size_t head_size = 0;
     // phase trace of the last launch (diagnostics)
     uint64_t* trace = nullptr;
     size_t trace_words = 0, trace_used = 0;
@@ -430,6 +435,7 @@ void bfi_smp_destroy(bfi_smp_ctx* ctx) {
         if (ctx->ws) (void)hipFree(ctx->ws);
         if (ctx->ctr) (void)hipFree(ctx->ctr);
         if (ctx->stage) (void)hipFree(ctx->stage);
+        if (ctx->head) (void)hipFree(ctx->head);
     }
     delete ctx;
 }
@@ -584,6 +590,60 @@ int bfi_smp_verify(bfi_smp_ctx* ctx, const void* d_logits, int dtype, int64_t n_
     c.out_acc = d_out_accepted;
     c.out_next = d_out_next;
     return run(ctx, c, (hipStream_t)stream);
+}
+
+namespace {
+
+// The output head into `out` (n_tok x n_out f32), the normalized rows in the context's head
+// workspace (whose first `lead` bytes the caller may use too).
+int run_head(bfi_smp_ctx* ctx, const float* x, const float* norm_w, int norm_per_row, float eps, const float* W,
+             int64_t n_tok, int64_t d, int64_t n_out, float* out, size_t lead, hipStream_t stream) {
+    if (!x || !norm_w || !W) return fail(ctx, BFI_SMP_EINVAL, "x, norm_w or W is NULL");
+    if (n_tok < 0 || d <= 0 || n_out <= 0 || n_tok > (1 << 20) || n_out > ((int64_t)1 << 31) / 64)
+        return fail(ctx, BFI_SMP_EINVAL, "head sizes out of range (n_tok %lld, d %lld, n_out %lld)", (long long)n_tok,
+                    (long long)d, (long long)n_out);
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+    const size_t need = align_up(lead, 256) + (size_t)n_tok * (size_t)d * sizeof(float);
+    if (need > ctx->head_size) {
+        if (ctx->head) (void)hipFree(ctx->head);
+        ctx->head = nullptr;
+        ctx->head_size = 0;
+        if (hipMalloc((void**)&ctx->head, need) != hipSuccess) {
+            ctx->head = nullptr;
+            return fail(ctx, BFI_SMP_ENOMEM, "head workspace allocation failed (%zu bytes)", need);
+        }
+        ctx->head_size = need;
+    }
+    float* xn = (float*)(ctx->head + align_up(lead, 256));
+    if (!out) out = (float*)ctx->head;
+    const int vec = (d % 4 == 0) && ((uintptr_t)W % 16 == 0);
+    const hipError_t e = bfi::launch_head(x, norm_w, norm_per_row, eps, W, n_tok, d, n_out, vec, xn, out, stream);
+    return e == hipSuccess ? BFI_SMP_OK : hip_fail(ctx, e, "head launch");
+}
+
+}  // namespace
+
+int bfi_smp_head(bfi_smp_ctx* ctx, const float* d_x, const float* d_norm_w, int norm_per_row, float eps,
+                 const float* d_w, int64_t n_tokens, int64_t n_embd, int64_t n_vocab, float* d_logits, void* stream) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    if (!d_logits) return fail(ctx, BFI_SMP_EINVAL, "d_logits is NULL");
+    return run_head(ctx, d_x, d_norm_w, norm_per_row, eps, d_w, n_tokens, n_embd, n_vocab, d_logits, 0,
+                    (hipStream_t)stream);
+}
+
+int bfi_smp_head_sample_rows(bfi_smp_ctx* ctx, const float* d_x, const float* d_norm_w, int norm_per_row, float eps,
+                             const float* d_w, int64_t n_tokens, int64_t n_embd, int64_t n_vocab,
+                             const bfi_smp_row_params* d_params, const uint32_t* d_hist, const int64_t* d_hist_off,
+                             const uint32_t* d_mask, int64_t mask_stride, const float* d_u, uint32_t* d_out,
+                             void* stream) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    const size_t lbytes = (size_t)(n_tokens > 0 ? n_tokens : 0) * (size_t)(n_vocab > 0 ? n_vocab : 0) * sizeof(float);
+    int rc = run_head(ctx, d_x, d_norm_w, norm_per_row, eps, d_w, n_tokens, n_embd, n_vocab, nullptr, lbytes,
+                      (hipStream_t)stream);
+    if (rc != BFI_SMP_OK) return rc;
+    return bfi_smp_sample_rows(ctx, ctx->head, BFI_SMP_F32, n_tokens, n_vocab, n_vocab, d_params, d_hist, d_hist_off,
+                               d_mask, mask_stride, d_u, d_out, stream);
 }
 
 int bfi_smp_sample_host(bfi_smp_ctx* ctx, const float* logits, int64_t n_vocab, const uint32_t* prev,

@@ -1,0 +1,120 @@
+// smp_head.hip — the output head that produces the sampler's logits on the device: the final
+// RMS norm and the lm_head product of the reference's `head` (crates/bfi-models/src/qwen3.rs:
+// 258-265, `rms_norm` then `matmul_q` over f32 weights, crates/bfi-core/src/cpu.rs:92-120 and
+// 498-514), with the reference's own rounding: every product and every addition of a dot
+// product is one f32 operation, added in index order from -0.0 (Rust's `Sum` of f32), so the
+// logits are bit-identical to the CPU backend's and the sampler downstream draws the same
+// token. That order rules out matrix cores (an MFMA sums in its own order): the product is a
+// register-tiled SIMT GEMM on the VALU, 2 instructions a term.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace bfi {
+
+namespace {
+
+constexpr int HN_BLOCK = 256;
+
+// One row per block: mean of squares summed by one lane in index order, then
+// out = x * (1 / sqrt(mean + eps)) * w elementwise (cpu.rs:92-120).
+__global__ __launch_bounds__(HN_BLOCK) void k_head_norm(const float* __restrict__ x, const float* __restrict__ w,
+                                                        int w_per_row, float eps, int64_t d,
+                                                        float* __restrict__ out) {
+    __shared__ float s_scale;
+    const int64_t r = blockIdx.x;
+    const float* xr = x + r * d;
+    const float* wr = w_per_row ? w + r * d : w;
+    if (threadIdx.x == 0) {
+        float s = -0.0f;
+        for (int64_t i = 0; i < d; i++) s = s + xr[i] * xr[i];
+        const float mean_sq = s / (float)d;
+        s_scale = 1.0f / __builtin_sqrtf(mean_sq + eps);
+    }
+    __syncthreads();
+    const float scale = s_scale;
+    for (int64_t i = threadIdx.x; i < d; i += HN_BLOCK) out[r * d + i] = xr[i] * scale * wr[i];
+}
+
+constexpr int HG_BO = 64;   // outputs (rows of W) a block
+constexpr int HG_BT = 64;   // tokens a block
+constexpr int HG_K = 16;    // inner-dimension chunk staged through LDS
+constexpr int HG_BLOCK = 256;
+
+// out[t][o] = sum over i in index order of W[o][i] * X[t][i]. A thread owns 4 outputs x 4
+// tokens; each chunk of 16 inner positions is staged transposed in LDS so a thread reads
+// its 4 weights and 4 inputs of one position as two 16-byte loads.
+__global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict__ W, const float* __restrict__ X,
+                                                        int64_t n_out, int64_t n_tok, int64_t d, int vec,
+                                                        float* __restrict__ out) {
+    __shared__ float4 Ws[HG_K][HG_BO / 4];
+    __shared__ float4 Xs[HG_K][HG_BT / 4];
+    const int tid = threadIdx.x;
+    const int to = tid % 16, tt = tid / 16;  // this thread: outputs 4 to.., tokens 4 tt..
+    const int64_t o0 = (int64_t)blockIdx.x * HG_BO, t0 = (int64_t)blockIdx.y * HG_BT;
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = -0.0f;
+    // staging: thread tid loads 4 consecutive inner positions of one row of the tile
+    const int lr = tid / 4, lc = (tid % 4) * 4;
+    const int64_t wrow = o0 + lr, xrow = t0 + lr;
+    for (int64_t k0 = 0; k0 < d; k0 += HG_K) {
+        float wv[4], xv[4];
+        if (vec && k0 + lc + 3 < d) {
+            const float4 a = wrow < n_out ? *reinterpret_cast<const float4*>(W + wrow * d + k0 + lc) : make_float4(0, 0, 0, 0);
+            const float4 b = xrow < n_tok ? *reinterpret_cast<const float4*>(X + xrow * d + k0 + lc) : make_float4(0, 0, 0, 0);
+            wv[0] = a.x, wv[1] = a.y, wv[2] = a.z, wv[3] = a.w;
+            xv[0] = b.x, xv[1] = b.y, xv[2] = b.z, xv[3] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int64_t i = k0 + lc + j;
+                wv[j] = (wrow < n_out && i < d) ? W[wrow * d + i] : 0.0f;
+                xv[j] = (xrow < n_tok && i < d) ? X[xrow * d + i] : 0.0f;
+            }
+        }
+        __syncthreads();  // (the previous chunk has been read)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            reinterpret_cast<float*>(&Ws[lc + j][0])[lr] = wv[j];
+            reinterpret_cast<float*>(&Xs[lc + j][0])[lr] = xv[j];
+        }
+        __syncthreads();
+        const int kn = d - k0 < HG_K ? (int)(d - k0) : HG_K;  // (a partial last chunk adds no padding)
+        for (int k = 0; k < kn; k++) {
+            const float4 a = Ws[k][to], b = Xs[k][tt];
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc[p][q] = acc[p][q] + av[p] * bv[q];
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int64_t t = t0 + tt * 4 + q;
+        if (t >= n_tok) continue;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int64_t o = o0 + to * 4 + p;
+            if (o < n_out) out[t * n_out + o] = acc[p][q];
+        }
+    }
+}
+
+}  // namespace
+
+// xn: n_tok * d floats of workspace; out: n_tok * n_out logits.
+// vec: d % 4 == 0 and W 16-byte aligned (the rows then load as 16-byte vectors).
+hipError_t launch_head(const float* x, const float* norm_w, int norm_per_row, float eps, const float* W,
+                       int64_t n_tok, int64_t d, int64_t n_out, int vec, float* xn, float* out, hipStream_t stream) {
+    if (n_tok <= 0 || n_out <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_head_norm, dim3((unsigned)n_tok), dim3(HN_BLOCK), 0, stream, x, norm_w, norm_per_row, eps, d, xn);
+    const dim3 grid((unsigned)((n_out + HG_BO - 1) / HG_BO), (unsigned)((n_tok + HG_BT - 1) / HG_BT));
+    hipLaunchKernelGGL(k_head_gemm, grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out);
+    return hipGetLastError();
+}
+
+}  // namespace bfi

@@ -194,6 +194,36 @@ int bfi_smp_sample_host(bfi_smp_ctx *ctx, const float *logits, int64_t n_vocab,
                         const uint32_t *prev, int64_t n_prev, const bfi_smp_row_params *params,
                         const uint32_t *allow_mask, float u, uint32_t *out_token);
 
+/* ---- device-resident logits: the output head ---------------------------- */
+
+/*
+ * The reference's `head` (crates/bfi-models/src/qwen3.rs:258-265: `rms_norm` then
+ * `matmul_q` with f32 weights, then `tutil::logit_rows`, tutil.rs:196-207) on the device, so
+ * a decode step's logits never leave HBM: d_x is [n_tokens, n_embd] f32 hidden rows, d_norm_w
+ * the output norm's weights ([n_embd], or [n_tokens, n_embd] when norm_per_row != 0,
+ * cpu.rs:98-115), d_w the lm_head weights [n_vocab, n_embd] f32, d_logits [n_tokens,
+ * n_vocab] f32. Rounding as the CPU backend's (cpu.rs:92-120, 498-514): the mean of squares
+ * and every dot product summed one f32 addition at a time in index order (from -0.0, Rust's
+ * f32 `Sum`), sqrt and 1/x correctly rounded, x * scale * w left to right; the logits are
+ * bit-identical to the reference's. Quantized lm_head weights (matmul_quant,
+ * cpu.rs:516-545) are not taken. Asynchronous on `stream`; n_tokens <= 2^20.
+ */
+int bfi_smp_head(bfi_smp_ctx *ctx, const float *d_x, const float *d_norm_w, int norm_per_row,
+                 float eps, const float *d_w, int64_t n_tokens, int64_t n_embd, int64_t n_vocab,
+                 float *d_logits, void *stream);
+
+/*
+ * bfi_smp_head into the context's workspace, then bfi_smp_sample_rows over those logits
+ * (row_stride n_vocab, f32): the fused step of a device-resident decode loop — hidden rows in,
+ * one u32 token a row out (4 bytes a row to read back instead of 4 n_vocab).
+ */
+int bfi_smp_head_sample_rows(bfi_smp_ctx *ctx, const float *d_x, const float *d_norm_w,
+                             int norm_per_row, float eps, const float *d_w, int64_t n_tokens,
+                             int64_t n_embd, int64_t n_vocab, const bfi_smp_row_params *d_params,
+                             const uint32_t *d_hist, const int64_t *d_hist_off,
+                             const uint32_t *d_mask, int64_t mask_stride, const float *d_u,
+                             uint32_t *d_out, void *stream);
+
 /* ---- host-side helpers (no GPU work) ------------------------------------ */
 
 /* xorshift64 step of `Rng::next_u64` (sample.rs:445-455); updates *state. */

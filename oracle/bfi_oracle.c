@@ -672,3 +672,32 @@ done:
     free(w);
     free(h);
 }
+
+/* ---- the output head (crates/bfi-core/src/cpu.rs) ---------------------------------------- */
+
+/* cpu.rs:92-120: mean_sq = sum(v * v) / d; scale = (mean_sq + eps).sqrt().recip();
+ * out = x * scale * w. */
+void orc_rms_norm(const float *x, const float *w, int w_per_row, float eps, int64_t n_rows, int64_t d,
+                  float *out) {
+    for (int64_t r = 0; r < n_rows; r++) {
+        const float *xs = x + r * d;
+        const float *ws = w_per_row ? w + r * d : w;
+        float s = -0.0f;
+        for (int64_t i = 0; i < d; i++) s = s + xs[i] * xs[i];
+        const float mean_sq = s / (float)d;
+        const float scale = 1.0f / sqrtf(mean_sq + eps);
+        for (int64_t i = 0; i < d; i++) out[r * d + i] = xs[i] * scale * ws[i];
+    }
+}
+
+/* cpu.rs:498-514: out[t][o] = dot(w[o], x[t]), the dot a sequential f32 sum of products. */
+void orc_matmul_f32(const float *w, const float *x, int64_t n_tokens, int64_t n_out, int64_t n_in,
+                    float *out) {
+    for (int64_t t = 0; t < n_tokens; t++)
+        for (int64_t o = 0; o < n_out; o++) {
+            const float *wr = w + o * n_in, *xr = x + t * n_in;
+            float s = -0.0f;
+            for (int64_t i = 0; i < n_in; i++) s = s + wr[i] * xr[i];
+            out[t * n_out + o] = s;
+        }
+}

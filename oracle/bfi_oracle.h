@@ -28,6 +28,9 @@
  *                                  closed form l - f*count in the tests
  *   packed allow-mask              equivalent to the id-union HashSet mask (sample.rs:331-337);
  *                                  pinned by comparing against orc_parse_id_union
+ *   orc_rms_norm, orc_matmul_f32   reference KATs rms_norm_ones / matmul_f32_identity
+ *                                  (cpu.rs:835-855) + numpy's sequential float32 accumulate
+ *                                  and correctly rounded sqrt on random rows
  */
 #ifndef BFI_ORACLE_H
 #define BFI_ORACLE_H
@@ -97,6 +100,15 @@ void orc_verify_seq(const void *rows, int dtype, int64_t n_vocab, int64_t row_st
                     const uint32_t *drafts, size_t draft_len, const uint32_t *masks,
                     int64_t mask_stride, const float *u_pairs, float u_bonus,
                     int32_t *accepted, uint32_t *next);
+
+/* The CPU backend's output head (crates/bfi-core/src/cpu.rs), which produces the logits the
+ * sampler reads (qwen3.rs:258-265 `head`): rms_norm (cpu.rs:92-120) and matmul_f32
+ * (cpu.rs:498-514 over scalar_dot_f32, simd.rs:61-63). Sums run one f32 addition at a time
+ * in index order from -0.0 (Rust's f32 `Sum`). w of rms_norm: [d] or [n_rows, d]. */
+void orc_rms_norm(const float *x, const float *w, int w_per_row, float eps, int64_t n_rows, int64_t d,
+                  float *out);
+void orc_matmul_f32(const float *w, const float *x, int64_t n_tokens, int64_t n_out, int64_t n_in,
+                    float *out);
 
 #ifdef __cplusplus
 }

@@ -123,12 +123,35 @@ def lib(path=None):
             I64, I64, P, ctypes.c_int, I64, P, P, P, P, I64, P, P, P, P, P, P, I64, P, P, ctypes.c_int
         ]
         L.orc_verify_seq.restype = None
+        L.orc_rms_norm.argtypes = [P, P, ctypes.c_int, ctypes.c_float, I64, I64, P]
+        L.orc_rms_norm.restype = None
+        L.orc_matmul_f32.argtypes = [P, P, I64, I64, I64, P]
+        L.orc_matmul_f32.restype = None
         L.orc_verify_seq.argtypes = [
             P, ctypes.c_int, I64, I64, P, P, ctypes.c_size_t, P, ctypes.c_size_t, P, I64, P,
             ctypes.c_float, P, P,
         ]
         _lib = L
     return _lib
+
+
+def rms_norm(x, w, eps: float, w_per_row: bool = False):
+    """cpu.rs:92-120 over rows of x (float32 [n, d])."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    n, d = x.shape
+    out = np.empty_like(x)
+    lib().orc_rms_norm(_ptr(x), _ptr(w), 1 if w_per_row else 0, ctypes.c_float(eps), n, d, _ptr(out))
+    return out
+
+
+def matmul_f32(w, x):
+    """cpu.rs:498-514: [n_tokens, n_out] = x @ w.T with sequential f32 dots."""
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty((x.shape[0], w.shape[0]), np.float32)
+    lib().orc_matmul_f32(_ptr(w), _ptr(x), x.shape[0], w.shape[0], w.shape[1], _ptr(out))
+    return out
 
 
 def _ptr(a):

@@ -1,0 +1,90 @@
+"""GPU parity of the output head (bfi_smp_head, include/bfi_sampler.h): the device logits equal
+the oracle's restatement of the reference's CPU head (rms_norm + matmul_f32, cpu.rs:92-120,
+498-514) bit for bit, at odd and unaligned shapes and at a Qwen3-0.6B-sized head
+(n_embd 1024, n_vocab 151936); and the fused head + sample step draws the oracle's tokens."""
+import numpy as np
+import pytest
+
+import bfi_smp
+import oracle as O
+import workloads
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def smp(gpu):
+    s = bfi_smp.Sampler(0)
+    yield s
+    s.close()
+
+
+def _dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def _case(rng, T, d, V, scale=1.0, per_row=False):
+    x = (rng.standard_normal((T, d)) * scale).astype(np.float32)
+    nw = rng.standard_normal((T, d) if per_row else d).astype(np.float32)
+    w = (rng.standard_normal((V, d)) / np.sqrt(d)).astype(np.float32)
+    return x, nw, w
+
+
+@pytest.mark.parametrize("T,d,V,per_row", [(1, 1, 1, False), (3, 5, 7, False), (2, 17, 130, True), (70, 64, 65, False),
+                                           (5, 130, 1000, False), (64, 256, 4099, True)])
+def test_head_matches_oracle_bitwise(smp, T, d, V, per_row):
+    import torch
+
+    rng = np.random.default_rng(T * 1000 + d)
+    x, nw, w = _case(rng, T, d, V, scale=float(rng.choice([1e-3, 1.0, 30.0])), per_row=per_row)
+    got = smp.head(_dev(x), _dev(nw), 1e-6, _dev(w), norm_per_row=per_row)
+    torch.cuda.synchronize()
+    want = O.matmul_f32(w, O.rms_norm(x, nw, 1e-6, w_per_row=per_row))
+    g = got.cpu().numpy()
+    bad = np.nonzero(g.view(np.uint32) != want.view(np.uint32))
+    assert bad[0].size == 0, (T, d, V, bad[0][:5], bad[1][:5])
+
+
+def test_head_unaligned_weights(smp):
+    """Weights starting 4 bytes into an allocation take the scalar loads."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    x, nw, w = _case(rng, 4, 64, 300)
+    big = torch.empty(w.size + 1, dtype=torch.float32, device="cuda:0")
+    big[1:] = _dev(w.reshape(-1))
+    wv = big[1:].view(300, 64)
+    got = smp.head(_dev(x), _dev(nw), 1e-5, wv)
+    torch.cuda.synchronize()
+    want = O.matmul_f32(w, O.rms_norm(x, nw, 1e-5))
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_qwen3_sized_head_and_fused_sampling(smp):
+    """n_embd 1024, n_vocab 151936, 4 rows (the oracle's head takes ~1 s a row): logits equal
+    bit for bit, and head_sample_rows draws the tokens the oracle samples from those logits."""
+    import torch
+
+    rng = np.random.default_rng(9)
+    T, d, V = 4, 1024, 151936
+    x, nw, w = _case(rng, T, d, V, scale=3.0)
+    w *= 8.0  # peaked rows: a few ids far above the rest
+    xd, nwd, wd = _dev(x), _dev(nw), _dev(w)
+    got = smp.head(xd, nwd, 1e-6, wd)
+    torch.cuda.synchronize()
+    logits = O.matmul_f32(w, O.rms_norm(x, nw, 1e-6))
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), logits.view(np.uint32))
+    rows = [dict(temperature=0.8, top_p=0.95), dict(temperature=0.0), dict(temperature=1.0, top_k=40, min_p=0.05),
+            dict(temperature=0.6, top_p=0.9, repeat_penalty=1.1)]
+    params = bfi_smp.params_array(rows)
+    hist = rng.integers(0, V, 32).astype(np.uint32)
+    off = np.array([0, 8, 16, 24, 32], np.int64)
+    u = rng.random(T).astype(np.float32)
+    out = torch.zeros(T, dtype=torch.int32, device="cuda:0")
+    pd = torch.from_numpy(params.view(np.uint8)).to("cuda:0")
+    smp.head_sample_rows(xd, nwd, 1e-6, wd, pd, _dev(u), out, _dev(hist.view(np.int32)), _dev(off))
+    torch.cuda.synchronize()
+    want = O.sample_rows(logits, params, hist, off, u)
+    assert out.cpu().numpy().astype(np.uint32).tolist() == [int(t) for t in want]
