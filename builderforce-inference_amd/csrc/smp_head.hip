@@ -15,19 +15,38 @@ namespace bfi {
 namespace {
 
 constexpr int HN_BLOCK = 256;
+constexpr int HN_CHUNK = 2048;  // floats of a row staged in LDS at a time
 
-// One row per block: mean of squares summed by one lane in index order, then
+// One row per block: the mean of squares summed by one lane in index order, over chunks of
+// the row staged in LDS by the block (the lane reads 16 floats a round trip), then
 // out = x * (1 / sqrt(mean + eps)) * w elementwise (cpu.rs:92-120).
 __global__ __launch_bounds__(HN_BLOCK) void k_head_norm(const float* __restrict__ x, const float* __restrict__ w,
                                                         int w_per_row, float eps, int64_t d,
                                                         float* __restrict__ out) {
+    __shared__ float4 buf[HN_CHUNK / 4];
     __shared__ float s_scale;
     const int64_t r = blockIdx.x;
     const float* xr = x + r * d;
     const float* wr = w_per_row ? w + r * d : w;
+    float s = -0.0f;  // (lane 0's running sum)
+    for (int64_t c0 = 0; c0 < d; c0 += HN_CHUNK) {
+        const int n = d - c0 < HN_CHUNK ? (int)(d - c0) : HN_CHUNK;
+        float* fb = reinterpret_cast<float*>(buf);
+        for (int i = threadIdx.x; i < n; i += HN_BLOCK) fb[i] = xr[c0 + i];
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int i = 0;
+            for (; i + 16 <= n; i += 16) {
+                const float4 a = buf[i / 4], b = buf[i / 4 + 1], c = buf[i / 4 + 2], e = buf[i / 4 + 3];
+                const float v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
+#pragma unroll
+                for (int k = 0; k < 16; k++) s = s + v[k] * v[k];
+            }
+            for (; i < n; i++) s = s + fb[i] * fb[i];
+        }
+        __syncthreads();  // (the chunk is summed before the next overwrites it)
+    }
     if (threadIdx.x == 0) {
-        float s = -0.0f;
-        for (int64_t i = 0; i < d; i++) s = s + xr[i] * xr[i];
         const float mean_sq = s / (float)d;
         s_scale = 1.0f / __builtin_sqrtf(mean_sq + eps);
     }
