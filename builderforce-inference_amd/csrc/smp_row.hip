@@ -842,28 +842,35 @@ __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, cons
         return L;
     }
     if (nv <= (uint32_t)SORTCAP) {
-        // medium: each key goes to its rank, the count of larger keys (keys are distinct:
-        // their ids differ); every thread ranks up to two keys in one pass over the list
-        static_assert(SORTCAP <= 2 * BLOCK, "two keys per thread");
+        // medium: runs of 64 keys sorted by one wave each in registers, then each key goes to
+        // its rank (keys are distinct: their ids differ): its place in its own run plus, in
+        // every other run, the keys above it (a branch-free binary search of the descending
+        // run; the last run's padding zeros rank below every key)
+        static_assert(SORTCAP <= 2 * BLOCK && SORTCAP <= LCAP, "two keys per thread, runs in the list");
         L.small = 1;
-        uint64_t* out = sm.grp;
-        const uint32_t i0 = (uint32_t)tid, i1 = (uint32_t)tid + BLOCK;
-        const uint64_t k0 = i0 < nv ? sm.list[i0] : ~0ull;  // (~0: no key, outranks nothing)
-        const uint64_t k1 = i1 < nv ? sm.list[i1] : ~0ull;
-        uint32_t r0 = 0, r1 = 0;
-        if (nv > (uint32_t)BLOCK) {
-#pragma unroll 4
-            for (uint32_t j = 0; j < nv; j++) {
-                const uint64_t kj = sm.list[j];
-                r0 += kj > k0 ? 1u : 0u;
-                r1 += kj > k1 ? 1u : 0u;
-            }
-        } else {
-#pragma unroll 8
-            for (uint32_t j = 0; j < nv; j++) r0 += sm.list[j] > k0 ? 1u : 0u;
+        const uint32_t nr = (nv + WAVE - 1) / WAVE;
+        for (uint32_t r = (uint32_t)wave_id(); r < nr; r += NWAVE) {
+            const uint32_t j = r * WAVE + (uint32_t)lane_id();
+            const uint64_t key = wave_sort_desc(j < nv ? sm.list[j] : 0ull);
+            sm.list[j] = key;
         }
-        if (i0 < nv) out[r0] = k0;
-        if (i1 < nv) out[r1] = k1;
+        __syncthreads();
+        uint64_t* out = sm.grp;
+        for (uint32_t i = (uint32_t)tid; i < nv; i += BLOCK) {
+            const uint64_t k = sm.list[i];
+            const uint32_t own = i / WAVE;
+            uint32_t rank = i % WAVE;
+#pragma unroll 4
+            for (uint32_t r = 0; r < nr; r++) {
+                if (r == own) continue;
+                const uint64_t* run = sm.list + r * WAVE;
+                uint32_t c = 0;
+#pragma unroll
+                for (uint32_t st = WAVE / 2; st > 0; st >>= 1) c += run[c + st - 1] > k ? st : 0u;
+                rank += c + (run[c] > k ? 1u : 0u);
+            }
+            out[rank] = k;
+        }
         __syncthreads();
         L.G = out;
         L.cum = reinterpret_cast<float*>(sm.list);
