@@ -37,7 +37,8 @@ constexpr int NSLOT = QVMAX * NWAVE;  // (vector, wave) slots of a chunk, in ind
 
 struct __align__(16) QuantSmem {
     uint64_t etab[32];       // glibc's expf table (EXP2_32), per-lane reads from LDS
-    uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids (two 16-bit halves a word)
+    uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids (two 16-bit halves a word);
+                                 // in a row's first chunk, later: the windows' terms
     uint32_t rq[QWIN + 1];   // per run: units
     uint32_t rhi[QWIN + 1];  // per run: its unit exponent + 150 (0: no element)
     float vs[NSLOT];         // per (vector, wave): sum of the terms
@@ -48,6 +49,7 @@ struct __align__(16) QuantSmem {
     uint32_t gbase;
 };
 static_assert(NSLOT <= WAVE, "one lane per (vector, wave) slot");
+static_assert(QWIN <= CHUNK_MAX / 2, "a first chunk's window terms fit the history counts' space");
 
 __device__ __forceinline__ uint32_t lds_min(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_min((BFI_LDS uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -79,10 +81,29 @@ template <bool BF16, int QV>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void k_quant(KArgs a) {  // 3 workgroups per CU
     __shared__ QuantSmem sm;
     const uint32_t G = gridDim.x, bid = blockIdx.x;
+    const uint32_t nc = (uint32_t)a.n_chunks;
+    // each XCD takes a contiguous block [L0, L0 + size) of the (row, chunk) order (its rows'
+    // chunks share its L2), and within it the rows' first chunks go first: their workgroups
+    // end with the walk of their items, the longest tail of the pass
     const uint32_t q8 = G / 8, r8 = G % 8, xcd = bid % 8, slot = bid / 8;
-    const uint32_t logical = xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot;
-    const int row = (int)(logical / (uint32_t)a.n_chunks);
-    const int chunk = (int)(logical % (uint32_t)a.n_chunks);
+    const uint32_t L0 = xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8;
+    const uint32_t size = q8 + (xcd < r8 ? 1u : 0u);
+    const uint32_t m0 = (L0 + nc - 1) / nc * nc;  // the block's first row start
+    const uint32_t n0 = m0 < L0 + size ? (L0 + size - m0 + nc - 1) / nc : 0u;  // row starts in it
+    uint32_t logical;
+    if (slot < n0) {
+        logical = m0 + slot * nc;
+    } else {
+        const uint32_t t = slot - n0;
+        if (t < m0 - L0 || nc == 1u) {
+            logical = L0 + t;
+        } else {
+            const uint32_t t2 = t - (m0 - L0);
+            logical = m0 + t2 / (nc - 1u) * nc + 1u + t2 % (nc - 1u);
+        }
+    }
+    const int row = (int)(logical / nc);
+    const int chunk = (int)(logical % nc);
     if (row >= a.n_rows) return;
     const uint32_t V = (uint32_t)a.V;
     const uint32_t c0 = (uint32_t)chunk * (uint32_t)a.chunk;
@@ -245,11 +266,20 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         else exact_terms<2, QV, EPV>(x, ev, C.T, C.rT, M, sm.etab);
     }
     uint32_t tk[QV];
+    if (egth > 0.0f) {  // (a masked element's term is 0: below the bound)
 #pragma unroll
-    for (int q = 0; q < QV; q++) {
-        tk[q] = 0;
+        for (int q = 0; q < QV; q++) {
+            tk[q] = 0;
 #pragma unroll
-        for (int e = 0; e < EPV; e++) tk[q] |= (ev[q][e] >= egth && x[q][e] > -__builtin_inff()) ? 1u << e : 0u;
+            for (int e = 0; e < EPV; e++) tk[q] |= ev[q][e] >= egth ? 1u << e : 0u;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < QV; q++) {
+            tk[q] = 0;
+#pragma unroll
+            for (int e = 0; e < EPV; e++) tk[q] |= x[q][e] > -__builtin_inff() ? 1u << e : 0u;
+        }
     }
 
     // the candidates' positions in the row's list: a block scan and one global count per
@@ -310,6 +340,8 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         constexpr int EBW = (EPV + 3) / 4;  // words of packed binades per vector
         uint32_t wmask = 0, zmask = 0;      // window and zero bits: bit q * EPV + e
         uint32_t eb[QV][EBW];
+        uint32_t vqs[QV];                   // per vector: its units, 2^23 + RN(t) each
+        uint32_t fbits = 0;                 // bit q: vector q lies in one binade
 #pragma unroll
         for (int q = 0; q < QV; q++) {
             // the vector as a whole: the interval from before its first element to after its
@@ -317,10 +349,11 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             const float vlo = fmaxf(vpre[q] * (1.0f - QEPS), vmx[q]);
             const float vhi = (vpre[q] + vsum[q]) * (1.0f + QEPS);
             const uint32_t velo = max(__float_as_uint(vlo) >> 23, 1u), vehi = max(__float_as_uint(vhi) >> 23, 1u);
-            uint32_t elo_e[EPV], wq = 0, zq = 0;
+            uint32_t elo_e[EPV], wq = 0, zq = 0, vq = 0;
             if (velo == vehi) {
 #pragma unroll
                 for (int e = 0; e < EPV; e++) elo_e[e] = velo;
+                fbits |= 1u << q;
             } else {
                 float A = vpre[q], L = vmx[q];
 #pragma unroll
@@ -340,17 +373,27 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             for (int e = 0; e < EPV; e++) {
                 const bool zero = !(ev[q][e] > 0.0f);
                 const float t = __builtin_ldexpf(ev[q][e], 150 - (int32_t)elo_e[e]);
-                const float qf = __builtin_rintf(t);
+                // t + 2^23 rounds t to an integer (ties to even) in the low mantissa bits, for
+                // t below 2^23 (larger t is a window, whose units are not used)
+                const float y = t + 8388608.0f;
+                const float qf = y - 8388608.0f;
                 const bool win = !zero & (((wq >> e) & 1u) | (fabsf(t - qf) == 0.5f) | !(t < 8388608.0f));
                 zq |= zero ? 1u << e : 0u;
                 wq = win ? wq | (1u << e) : wq & ~(1u << e);
+                vq += __float_as_uint(y);
             }
+            vqs[q] = vq - (uint32_t)EPV * 0x4B000000u;
+            if (velo == vehi) {
 #pragma unroll
-            for (int i = 0; i < EBW; i++) {
-                uint32_t wd = 0;
+                for (int i = 0; i < EBW; i++) eb[q][i] = (velo & 0xFFu) * 0x01010101u;
+            } else {
 #pragma unroll
-                for (int e = 4 * i; e < EPV && e < 4 * i + 4; e++) wd |= (elo_e[e] & 0xFFu) << (8 * (e - 4 * i));
-                eb[q][i] = wd;
+                for (int i = 0; i < EBW; i++) {
+                    uint32_t wd = 0;
+#pragma unroll
+                    for (int e = 4 * i; e < EPV && e < 4 * i + 4; e++) wd |= (elo_e[e] & 0xFFu) << (8 * (e - 4 * i));
+                    eb[q][i] = wd;
+                }
             }
             wmask |= wq << (q * EPV);
             zmask |= zq << (q * EPV);
@@ -363,12 +406,18 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         BFI_TRACE(a, tb, 4);
         // window positions in index order
         uint32_t wpre[QV];
+        if (__ballot(wmask != 0u)) {
 #pragma unroll
-        for (int q = 0; q < QV; q++) {
-            const uint32_t c = (uint32_t)__popc((wmask >> (q * EPV)) & em);
-            const uint32_t incl = wave_scan_incl(c, 0u, [](uint32_t u, uint32_t v) { return u + v; });
-            if (lane == WAVE - 1) sm.vc[q * NWAVE + w] = incl;
-            wpre[q] = incl - c;
+            for (int q = 0; q < QV; q++) {
+                const uint32_t c = (uint32_t)__popc((wmask >> (q * EPV)) & em);
+                const uint32_t incl = wave_scan_incl(c, 0u, [](uint32_t u, uint32_t v) { return u + v; });
+                if (lane == WAVE - 1) sm.vc[q * NWAVE + w] = incl;
+                wpre[q] = incl - c;
+            }
+        } else {  // (most waves: no window)
+#pragma unroll
+            for (int q = 0; q < QV; q++) wpre[q] = 0u;
+            if (lane < QV) sm.vc[lane * NWAVE + w] = 0u;
         }
         __syncthreads();
         uint32_t nwin;
@@ -396,6 +445,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
 #pragma unroll
                     for (int e = 1; e < EPV; e++) ee = e == i ? ev[q][e] : ee;
                     *reinterpret_cast<uint2*>(&items[pos]) = make_uint2(id0 + (uint32_t)i, __float_as_uint(ee));
+                    if (chunk == 0) sm.hc[pos] = __float_as_uint(ee);  // (for the walk below)
                     pos++;
                 }
             }
@@ -415,14 +465,20 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                 const uint32_t wmq = (wmask >> (q * EPV)) & em, zmq = (zmask >> (q * EPV)) & em;
                 if (wmq == 0u) {
                     if (zmq == em) continue;
-                    uint32_t vq = 0, vh = 0, vl = 0xFFu;
+                    // (a vector without windows: its units were summed where it was classified;
+                    // in one binade, that binade, else its nonzero elements' lowest and highest)
+                    const uint32_t vq = vqs[q];
+                    uint32_t vh = eb[q][0] & 0xFFu, vl = vh;
+                    if (!((fbits >> q) & 1u)) {
+                        vh = 0;
+                        vl = 0xFFu;
 #pragma unroll
-                    for (int e = 0; e < EPV; e++) {
-                        const bool z = (zmq >> e) & 1u;
-                        const uint32_t b = elo_of(q, e);
-                        vq += z ? 0u : units_at(q, e, b);
-                        vh = z ? vh : max(vh, b);
-                        vl = z ? vl : min(vl, b);
+                        for (int e = 0; e < EPV; e++) {
+                            const bool z = (zmq >> e) & 1u;
+                            const uint32_t b = elo_of(q, e);
+                            vh = z ? vh : max(vh, b);
+                            vl = z ? vl : min(vl, b);
+                        }
                     }
                     const uint32_t k = wpre[q];
                     if (have && k != key) {
@@ -508,7 +564,6 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         }
         qflags = flags;
         qn = nwin;
-        if (a.trace && tid == 0) a.trace[tb + 6] = nwin;  // diagnostics: windows
     }
 
     // the candidates of the kept set into the row's list, as (id, e)
@@ -537,26 +592,39 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
     }
     // a row's first chunk starts from 0: its items are walked here, off the row kernel's
     // path, and become one, the exact sum after the chunk (if the walk needs no re-stream)
+    uint64_t tsync = 0;  // diagnostics
     if (chunk == 0 && !trivial && qflags == 0u) {
         __threadfence_block();
         __syncthreads();
+        if (a.trace && tid == 0) tsync = wall_clock64() - a.trace[tb];
         if (w == 0) {
-            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            // a serial walk beside the VALU-heavy waves of the CU's other workgroups: it goes
+            // first in the SIMD's issue arbitration
+            __builtin_amdgcn_s_setprio(3);
             uint32_t m = 0u;
             int32_t ue = -149;
             const uint32_t n = qn + 1u;
+            // the items from LDS: the runs' tables and the windows' terms (the history
+            // counts' space); an element's index only has to be below V here
             const uint32_t hit = chain_run(
                 [&](uint32_t j) {
-                    const u32x4 v = *(const BFI_GLB u32x4*)(items + j);
-                    return QItem{v.x, __uint_as_float(v.y), v.z, (int32_t)v.w};
+                    const uint32_t hi = sm.rhi[j];
+                    const bool el = j < qn;
+                    return QItem{el ? 0u : QI_NONE, el ? __uint_as_float(sm.hc[j]) : 0.0f, sm.rq[j],
+                                 hi ? (int32_t)hi - 150 : -(int32_t)UE_BIAS};
                 },
                 0u, n, (uint32_t)a.V, m, ue);
             if (hit == n && lane == 0) {
                 items[0] = QItem{QI_SET, state_value(m, ue), 0u, -(int32_t)UE_BIAS};
                 head->nwin = 0u;
             }
+            __builtin_amdgcn_s_setprio(0);
         }
     }
+    // diagnostics: the windows (bits 0-19), and the times from the start stamp to the first
+    // chunk's walk (bits 20-41) and to here (bits 42-63)
+    if (a.trace && tid == 0)
+        a.trace[tb + 6] = (uint64_t)qn | ((tsync & 0x3FFFFFull) << 20) | (((wall_clock64() - a.trace[tb]) & 0x3FFFFFull) << 42);
 }
 
 // `vec` is the streaming pass's 16-byte vectors per thread at 256 threads (its chunk); this
