@@ -355,7 +355,9 @@ int run(bfi_smp_ctx* ctx, const Call& c, hipStream_t stream, const Fixed* fixed 
     a.qcap = (int32_t)qcap_of(s);
     a.trace = nullptr;
     if (ctx->tracing && !fixed) {
-        size_t words = (size_t)c.n_rows * s.n_chunks * 8 + (size_t)c.n_rows * 16;
+        // the quantizing pass's workgroups (8 words), the rows (16), the streaming pass's
+        // workgroups (8)
+        size_t words = (size_t)c.n_rows * s.n_chunks * 16 + (size_t)c.n_rows * 16;
         if (words > ctx->trace_words) {
             if (ctx->trace) (void)hipFree(ctx->trace);
             ctx->trace = nullptr;

@@ -35,7 +35,7 @@ constexpr int HB_CBITS = 20;              // histogram bins: count bits (a chunk
 static_assert(CHUNK_MAX < (1 << HB_CBITS), "bin counts");
 constexpr int NGRID = 512;                // gather-bound grid: bounds -g/8 log2-units, g < NGRID
 constexpr double MFIX = 1099511627776.0;  // 2^40: fixed point of the grid masses
-static_assert(NGRID * 3 <= CHUNK_MAX / 2, "the grids reuse the count array");
+static_assert(NGRID * 3 + NCMAX * 3 <= CHUNK_MAX / 2, "the grids and the chunk factors reuse the count array");
 
 // The candidate bound from the chunks' histograms: bin j of chunk c holds the count and the
 // mass (terms relative to the chunk maximum) of the elements j/4 .. (j+1)/4 log2-units below
@@ -46,8 +46,23 @@ static_assert(NGRID * 3 <= CHUNK_MAX / 2, "the grids reuse the count array");
 // theta_g whose lower bounds reach k (top-k) or the top-p share of an upper bound on the
 // normalizer with margins for the reference's rounding (sample.rs:392-409). Every kept
 // element lies above it.
+constexpr int HPER = 16;  // histogram words a thread loads at a time
+
+// The first HPER * BLOCK words of a row's chunk histograms (the last bin of each is not used):
+// loaded at the start of the row finisher, beside its other loads.
+__device__ __forceinline__ void hist_prefetch(const KArgs& a, int row, uint64_t (&hv)[HPER]) {
+    const int tid = threadIdx.x;
+    const int nc = a.n_chunks;
+    const uint64_t* vh = reinterpret_cast<const uint64_t*>(a.vhist + (int64_t)row * nc * 2 * HBINS);
+#pragma unroll
+    for (int r = 0; r < HPER; r++) {
+        const int idx = r * BLOCK + tid;
+        hv[r] = (idx < nc * HBINS && (idx % HBINS) != HBINS - 1) ? ld_dev64(vh + idx) : 0ull;
+    }
+}
+
 __device__ __forceinline__ float gather_bound(const KArgs& a, StreamSmem& sm, const RowCtx& C, float xmax,
-                                              double S_hi) {
+                                              double S_hi, const uint64_t (&hv0)[HPER]) {
     const int tid = threadIdx.x;
     const int nc = a.n_chunks;
     uint32_t* CL = sm.hc;
@@ -58,17 +73,30 @@ __device__ __forceinline__ float gather_bound(const KArgs& a, StreamSmem& sm, co
     }
     __syncthreads();
     const float eps = 0x1p-8f;
-    // the chunks' histograms, 16 bins per thread in flight together
-    constexpr int PER = 16;
+    // per chunk: its maximum's offset below the row's in grid units, and the factor that
+    // takes its bins' masses (relative to its maximum) to the row's scale, lowered for the
+    // estimates' errors (one exp2 per chunk, not per bin)
+    double* CS = reinterpret_cast<double*>(sm.hc + NGRID * 3);
+    float* CO = reinterpret_cast<float*>(CS + NCMAX);
+    if (tid < nc) {
+        const float o = (xmax - sm.xm[tid]) * C.rTl;
+        CO[tid] = 8.0f * o + 8.0f * eps;
+        CS[tid] = C.pmode ? exp2(-(double)o - (double)eps) * (1.0 - 0x1p-9) * MFIX : 0.0;
+    }
+    __syncthreads();
+    // the chunks' histograms, HPER bins per thread in flight together (the first batch
+    // prefetched)
+    constexpr int PER = HPER;
     const uint32_t* vh = a.vhist + (int64_t)C.row * nc * 2 * HBINS;
     for (int b0 = 0; b0 < nc * HBINS; b0 += PER * BLOCK) {
         uint64_t hv[PER];
 #pragma unroll
         for (int r = 0; r < PER; r++) {
             const int idx = b0 + r * BLOCK + tid;
-            hv[r] = (idx < nc * HBINS && (idx % HBINS) != HBINS - 1)
-                        ? ld_dev64(reinterpret_cast<const uint64_t*>(vh) + idx)
-                        : 0ull;
+            hv[r] = b0 == 0 ? hv0[r]
+                            : (idx < nc * HBINS && (idx % HBINS) != HBINS - 1)
+                                  ? ld_dev64(reinterpret_cast<const uint64_t*>(vh) + idx)
+                                  : 0ull;
         }
 #pragma unroll
         for (int r = 0; r < PER; r++) {
@@ -77,15 +105,11 @@ __device__ __forceinline__ float gather_bound(const KArgs& a, StreamSmem& sm, co
             if (!cnt && !(ms > 0.0f)) continue;
             const int idx = b0 + r * BLOCK + tid;
             const int c = idx / HBINS, j = idx % HBINS;
-            const float o = (xmax - sm.xm[c]) * C.rTl;
-            const float glo = ceilf(8.0f * o + (float)(8 * (j + 1) / HBIN_PER_LOG2) + 8.0f * eps);
+            const float glo = ceilf(CO[c] + (float)(8 * (j + 1) / HBIN_PER_LOG2));
             if (glo < (float)NGRID) {
                 const int g = (int)glo;
                 if (cnt) lds_add(&CL[g], cnt);
-                if (ms > 0.0f) {
-                    const double m = (double)ms * exp2(-(double)o - (double)eps) * (1.0 - 0x1p-9);
-                    lds_add64(&ML[g], (uint64_t)(m * MFIX));
-                }
+                if (ms > 0.0f) lds_add64(&ML[g], (uint64_t)((double)ms * CS[c]));
             }
         }
     }
@@ -122,11 +146,15 @@ __device__ __forceinline__ float gather_bound(const KArgs& a, StreamSmem& sm, co
 }
 
 // The row results from all chunks (the last workgroup of the row; every thread calls it).
-__device__ __forceinline__ void finish_row(const KArgs& a, StreamSmem& sm, int row) {
-    const RowCtx C = make_ctx(a, row);
+__device__ __forceinline__ void finish_row(const KArgs& a, StreamSmem& sm, const RowCtx& C) {
+    const int row = C.row;
     const int tid = threadIdx.x;
     const int nc = a.n_chunks;
     static_assert(NCMAX <= BLOCK, "one chunk per thread");
+    // the histograms the candidate bound reads, in flight with the chunk results
+    const bool bound = !C.greedy && (C.kmode || C.pmode) && !(C.min_p >= 0x1p-10f) && !C.pen_hash;
+    uint64_t hv[HPER];
+    if (bound) hist_prefetch(a, row, hv);
     ChunkPart P;
     P.m = -__builtin_inff();
     P.xm = -__builtin_inff();
@@ -172,8 +200,7 @@ __device__ __forceinline__ void finish_row(const KArgs& a, StreamSmem& sm, int r
         R.S_apx = (float)tot;
         const bool list_mode = C.kmode || C.pmode || C.mmode;
         float th = -__builtin_inff();
-        if ((C.kmode || C.pmode) && !(C.min_p >= 0x1p-10f) && !C.pen_hash && R.xmax > -__builtin_inff())
-            th = gather_bound(a, sm, C, R.xmax, tot * (1.0 + 1e-4));
+        if (bound && R.xmax > -__builtin_inff()) th = gather_bound(a, sm, C, R.xmax, tot * (1.0 + 1e-4), hv);
         if (C.mmode) th = fmaxf(th, log2f(C.min_p) - 0x1p-6f);
         if (list_mode) R.th = th;
     }
@@ -187,6 +214,12 @@ __device__ __forceinline__ void finish_row(const KArgs& a, StreamSmem& sm, int r
 template <bool BF16, int VEC, bool FULL>
 __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int row, int chunk, uint32_t c0,
                                              uint32_t c1);
+
+// Phase timestamp of a workgroup (diagnostics): words after the quantizing pass's and the rows'.
+#define BFI_STRACE(a, row, chunk, i)                                                                  \
+    BFI_TRACE(a, (int64_t)(a).n_rows * (a).n_chunks * 8 + (int64_t)(a).n_rows * 16 +                 \
+                     ((int64_t)(row) * (a).n_chunks + (chunk)) * 8,                                  \
+              i)
 
 template <bool BF16, int VEC>
 __global__ __launch_bounds__(BLOCK, 5) void k_stream(KArgs a) {
@@ -221,6 +254,7 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
     // (scalar loads that queue behind other workgroups' traffic) arrive meanwhile. The
     // allow-mask words go before the logits, so the pass can start on the first vector while
     // the rest are in flight; the history ids go between the two halves of the logits.
+    BFI_STRACE(a, row, chunk, 0);
     const HistView hv = row_history(a, row);
     const uint32_t* mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
     uint32_t mwd[VEC];
@@ -336,6 +370,7 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
         }
         m = mn;
     }
+    BFI_STRACE(a, row, chunk, 1);
     // the wave's (max, sum), then the chunk's from the NWAVE wave results (one barrier)
     {
         const float mw = wave_max(m);
@@ -364,6 +399,7 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
         for (int i = tid; i < 2 * HBINS; i += BLOCK) sm.hc[i] = 0u;
     }
     __syncthreads();
+    BFI_STRACE(a, row, chunk, 2);
     float lm = sm.wm[0];
 #pragma unroll
     for (int i = 1; i < NWAVE; i++) lm = fmaxf(lm, sm.wm[i]);
@@ -415,6 +451,7 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
         uint32_t* dst = a.vhist + ((int64_t)row * a.n_chunks + chunk) * 2 * HBINS;
         for (int i = tid; i < 2 * HBINS; i += BLOCK) st_dev(dst + i, sm.hc[i]);
     }
+    BFI_STRACE(a, row, chunk, 3);
     if (tid < 4) {
         const uint64_t* pw = reinterpret_cast<const uint64_t*>(&part);
         uint64_t v = pw[0];
@@ -430,8 +467,10 @@ __device__ __forceinline__ void stream_chunk(const KArgs& a, StreamSmem& sm, int
     __syncthreads();
     if (tid == 0) sm.last = glb_add(&a.arrive[row], 1u) == (uint32_t)(a.n_chunks - 1) ? 1u : 0u;
     __syncthreads();
+    BFI_STRACE(a, row, chunk, 4);
     if (!sm.last) return;
-    finish_row(a, sm, row);
+    finish_row(a, sm, C);
+    BFI_STRACE(a, row, chunk, 5);
 }
 
 // ---- launch ----------------------------------------------------------------------------
