@@ -776,45 +776,54 @@ __device__ __forceinline__ uint64_t make_key(float p, uint32_t id, bool idxmode)
 // Turns the N gathered (id, e) entries of the row's list (e: the exact term) into keys, keeps
 // those with p >= p_lo (> 0), compacted (LDS, then the row's spill area from 2V), and groups
 // them by bucket; at most WAVE keys are sorted by one wave instead. Every thread calls it.
+// pf: the N (<= BLOCK) entries are already in sm.list[0, N) (fetched at the row's start).
 __device__ __forceinline__ ListInfo build_list(const KArgs& a, RowSmem& sm, const RowCtx& C, uint32_t N, float M,
-                                               float S, float p_lo, bool idxmode) {
+                                               float S, float p_lo, bool idxmode, bool pf = false) {
     const int tid = threadIdx.x;
     const uint64_t* src = a.spill + (int64_t)C.row * 4 * a.V;
     uint64_t* ovf = a.spill + (int64_t)C.row * 4 * a.V + 2 * (int64_t)a.V;
     N = min(N, (uint32_t)a.V);
+    uint64_t ent0 = 0;
+    if (pf) ent0 = (uint32_t)tid < N ? sm.list[tid] : 0ull;  // (read before any key lands)
     if (tid == 0) sm.misc[MS_NV] = 0u;
     __syncthreads();
     uint32_t hmax = 0u, hmin = 0xFFFFFFFFu;
     uint64_t kmax = 0;
     constexpr int BB = 8;  // entries loaded at once (global memory latency)
-    for (uint32_t j0 = tid; j0 < N; j0 += BB * BLOCK) {
-        uint64_t ent[BB];
-#pragma unroll
-        for (int i = 0; i < BB; i++) {
-            const uint32_t j = j0 + (uint32_t)(i * BLOCK);
-            ent[i] = j < N ? src[j] : 0ull;
+    // entry j (in range or not: every lane of a wave takes part) into the list as a key
+    auto take = [&](uint64_t ent, bool in) {
+        const uint32_t id = (uint32_t)(ent >> 32);
+        const float p = exact_p(__uint_as_float((uint32_t)ent), S);
+        const bool valid = in && p > 0.0f && p >= p_lo;
+        const uint64_t key = make_key(p, id, idxmode);
+        const uint64_t bal = __ballot(valid);
+        if (!bal) return;
+        const int leader = __ffsll((unsigned long long)bal) - 1;
+        uint32_t base = 0;
+        if (lane_id() == leader) base = lds_add(&sm.misc[MS_NV], (uint32_t)__popcll(bal));
+        base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
+        if (valid) {
+            const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
+            if (pos < (uint32_t)LCAP) sm.list[pos] = key;
+            else ovf[pos] = key;
+            const uint32_t hi = (uint32_t)(key >> 32);
+            hmax = max(hmax, hi);
+            hmin = min(hmin, hi);
+            kmax = key > kmax ? key : kmax;
         }
+    };
+    if (pf) {
+        take(ent0, (uint32_t)tid < N);
+    } else {
+        for (uint32_t j0 = tid; j0 < N; j0 += BB * BLOCK) {
+            uint64_t ent[BB];
 #pragma unroll
-        for (int i = 0; i < BB; i++) {
-            const uint32_t id = (uint32_t)(ent[i] >> 32);
-            const float p = exact_p(__uint_as_float((uint32_t)ent[i]), S);
-            const bool valid = j0 + (uint32_t)(i * BLOCK) < N && p > 0.0f && p >= p_lo;
-            const uint64_t key = make_key(p, id, idxmode);
-            const uint64_t bal = __ballot(valid);
-            if (!bal) continue;
-            const int leader = __ffsll((unsigned long long)bal) - 1;
-            uint32_t base = 0;
-            if (lane_id() == leader) base = lds_add(&sm.misc[MS_NV], (uint32_t)__popcll(bal));
-            base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
-            if (valid) {
-                const uint32_t pos = base + (uint32_t)__popcll(bal & lanes_below());
-                if (pos < (uint32_t)LCAP) sm.list[pos] = key;
-                else ovf[pos] = key;
-                const uint32_t hi = (uint32_t)(key >> 32);
-                hmax = max(hmax, hi);
-                hmin = min(hmin, hi);
-                kmax = key > kmax ? key : kmax;
+            for (int i = 0; i < BB; i++) {
+                const uint32_t j = j0 + (uint32_t)(i * BLOCK);
+                ent[i] = j < N ? src[j] : 0ull;
             }
+#pragma unroll
+            for (int i = 0; i < BB; i++) take(ent[i], j0 + (uint32_t)(i * BLOCK) < N);
         }
     }
     __threadfence_block();
@@ -1709,12 +1718,12 @@ __device__ __noinline__ ArgMax row_max(const StreamArgs Ain) {
 constexpr int QSTAGE = (int)(sizeof(RowSmem::grp) / (sizeof(QItem)));  // items the grouped-key array holds
 
 
-// The chunk heads: item offsets and flags into LDS; returns the item count. Every thread.
-__device__ __forceinline__ uint32_t chain_heads(const QHead* heads, int nc, RowSmem& sm) {
+// The chunk heads (thread c holds chunk c's): item offsets and flags into LDS; returns the
+// item count. Every thread.
+__device__ __forceinline__ uint32_t chain_heads(const QHead& h, int nc, RowSmem& sm) {
     const int tid = threadIdx.x;
     uint32_t n = 0;
     if (tid < nc) {
-        const QHead h = heads[tid];
         sm.cflag[tid] = h.flags;
         n = (h.flags & QF_EXACT) ? 1u : h.nwin + 1u;
     }
@@ -1951,8 +1960,16 @@ template <bool BF16>
 __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int row) {
     const int tid = threadIdx.x;
     const RowCtx C = make_ctx(a, row);
-    if (!C.active) return;  // a verify row past its draft
     const int nc = a.n_chunks;
+    // issued first, beside the row's other loads: the quantizing pass's chunk heads and, for a
+    // short list (one entry a thread), its gathered candidates (both only read on its path)
+    const uint32_t ncand = ld_uniform(a.rowcnt + row);
+    const bool pf = ncand <= (uint32_t)BLOCK;
+    uint64_t pfe = 0;
+    if (pf && (uint32_t)tid < ncand) pfe = a.spill[(int64_t)row * 4 * a.V + tid];
+    QHead hd{0u, 0u};
+    if (tid < nc) hd = a.qhead[(int64_t)row * nc + tid];
+    if (!C.active) return;  // a verify row past its draft
     const uint32_t V = (uint32_t)a.V;
     BFI_RTRACE(a, C, 0);
     // 1. the row results of the streaming pass: maximum, argmax keys, candidate bound
@@ -2006,9 +2023,13 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
     // 2. the normalizer (sample.rs:381-386) and the candidate list
     float S;
     uint32_t N = 0;
+    bool listpf = false;  // the list's entries are in sm.list (the quantizing pass's, prefetched)
     if (quant_row(C, M)) {
         // the quantizing pass's chunk summaries, chained; it gathered the candidates
-        const uint32_t total = chain_heads(a.qhead + (int64_t)row * nc, nc, sm);
+        const uint32_t total = chain_heads(hd, nc, sm);
+        // (the list array is free until the list is built)
+        listpf = pf && list_mode;
+        if (listpf && (uint32_t)tid < ncand) sm.list[tid] = pfe;
         BFI_RTRACE(a, C, 10);
         ChainIO io{0.0f, 0u, 0u, 0u};
         uint32_t nfb = 0;
@@ -2035,7 +2056,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
         S = io.s;
         BFI_RTRACE(a, C, 11);
         if (a.trace && tid == 0) a.trace[(int64_t)a.n_rows * nc * 8 + (int64_t)row * 16 + 9] = nfb;
-        N = list_mode ? ld_uniform(a.rowcnt + row) : 0u;
+        N = list_mode ? ncand : 0u;
     } else {
         // the whole row streamed exactly, gathering the candidates on the way
         if (!tabs) {
@@ -2059,7 +2080,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
     if (sorted) {
         for (int attempt = 0; attempt < 2; attempt++) {
             const float p_lo = exhaustive ? 0.0f : (float)(exp2((double)th) / (double)S * (1.0 + 0x1p-20));
-            const ListInfo L = build_list(a, sm, C, N, M, S, p_lo, false);
+            const ListInfo L = build_list(a, sm, C, N, M, S, p_lo, false, listpf && attempt == 0);
             if (!L.small) bucket_units(L, sm, 0ull);
             BFI_RTRACE(a, C, 5);
             // top-p (sample.rs:397-409); a sampled row's walks over a small list keep the
@@ -2186,7 +2207,7 @@ __device__ __forceinline__ void row_main(const KArgs& a, RowSmem& sm, const int 
     const float thresh = C.mmode ? C.min_p * p1 : 0.0f;
     if (C.mmode && thresh > 0.0f) {
         // min-p alone: the kept elements in index order (sample.rs:411-414)
-        const ListInfo L = build_list(a, sm, C, N, M, S, thresh, true);
+        const ListInfo L = build_list(a, sm, C, N, M, S, thresh, true, listpf);
         if (L.n == 0) {
             put_stats(a, C, M, S, 0.0f, 2.0f);
             finish_token(a, sm, C, raw_tok);
