@@ -598,9 +598,6 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
         __syncthreads();
         if (a.trace && tid == 0) tsync = wall_clock64() - a.trace[tb];
         if (w == 0) {
-            // a serial walk beside the VALU-heavy waves of the CU's other workgroups: it goes
-            // first in the SIMD's issue arbitration
-            __builtin_amdgcn_s_setprio(3);
             uint32_t m = 0u;
             int32_t ue = -149;
             const uint32_t n = qn + 1u;
@@ -618,7 +615,6 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                 items[0] = QItem{QI_SET, state_value(m, ue), 0u, -(int32_t)UE_BIAS};
                 head->nwin = 0u;
             }
-            __builtin_amdgcn_s_setprio(0);
         }
     }
     // diagnostics: the windows (bits 0-19), and the times from the start stamp to the first
