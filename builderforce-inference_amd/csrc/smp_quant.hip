@@ -9,7 +9,7 @@
 // before this chunk (both from the streaming pass's row finisher), a workgroup predicts the
 // running sum before each of its elements, and so the binade each addition lands in. The
 // prediction is an interval: the prefix of the exact terms widened by QEPS relative both
-// ways (several times the f32 sum's largest drift from the exact one on the benchmark rows),
+// ways (about twice the f32 sum's largest drift from the exact one on the benchmark rows),
 // raised to the largest term added so far (the f32 sum never falls below any of its terms).
 // An element is "certain" when the interval before its addition and the one after lie in
 // one binade; its units are then RN(e / u) at that binade, exactly. The others ("windows":
@@ -30,7 +30,11 @@
 
 namespace bfi {
 
-constexpr float QEPS = 0x1p-9f;   // relative width of the running-sum prediction
+// Relative width of the running-sum prediction: about twice the largest drift of the f32
+// sum from the exact one on the benchmark rows (2^-10.9). A wider margin lists more windows
+// (bands near a binade boundary grow with it); a narrower one lets more rows outrun their
+// prediction, whose chunks are then streamed exactly (time, never the result).
+constexpr float QEPS = 0x1p-10f;
 constexpr uint32_t UE_BIAS = 1024u;
 constexpr int QVMAX = 4;             // 16-byte vectors per thread
 constexpr int NSLOT = QVMAX * NWAVE;  // (vector, wave) slots of a chunk, in index order
