@@ -1453,9 +1453,40 @@ __device__ __forceinline__ WalkOut walk(const ListInfo L, float th, uint32_t R, 
     w.r = 0;
     bool stopped = false;
     if (L.small) {
-        if (wave_id() == 0)
-            for (uint32_t j0 = 0; j0 < L.n && !stopped; j0 += WAVE)
+        if (wave_id() == 0) {
+            // the first WAVE keys as real f32 additions, one after another in straight-line code
+            // (lane j's key read by every lane, the sum after it kept by lane j): at the head of
+            // a descending list the running sum is small against its terms and leaves its
+            // binade or meets a tie every few keys, each a round of the wave-wide walk below
+            const uint32_t n0 = min(L.n, (uint32_t)WAVE);
+            const uint64_t kl = (uint32_t)lane < n0 ? L.G[lane] : 0ull;
+            const bool valid = (uint32_t)lane < n0 && kl != excl;
+            const float pl = valid ? key_p(kl, idxmode) : 0.0f;
+            float sl = 0.0f, sh = 0.0f;  // (adding 0 for the other lanes leaves the sum as it is)
+#pragma unroll
+            for (int j = 0; j < WAVE; j++) {
+                sh = sh + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl), j));
+                sl = lane == j ? sh : sl;
+            }
+            const uint64_t vb = __ballot(valid);
+            const uint32_t ci = (uint32_t)__popcll(vb & lanes_below()) + (valid ? 1u : 0u);  // rank + 1
+            const float thr = fmaxf(th, 0.0f);  // (the wave-wide walk's threshold units)
+            const uint64_t eb = __ballot(valid && (sl >= thr || ci >= R));
+            const int js = eb ? __ffsll((unsigned long long)eb) - 1 : WAVE;
+            if (cum && valid && lane <= js) cum[ci - 1u] = sl;
+            if (eb) {
+                const float s_j = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sl), js));
+                const uint64_t k_j = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(kl >> 32), js) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kl, js);
+                o = WalkOut{s_j, (uint32_t)__builtin_amdgcn_readlane((int)ci, js) - 1u, k_j, s_j >= thr ? 1 : 2};
+                stopped = true;
+            } else {
+                walk_set(w, sh, th);
+                w.r = (uint32_t)__popcll(vb);
+            }
+            for (uint32_t j0 = n0; j0 < L.n && !stopped; j0 += WAVE)
                 stopped = walk_elems(w, j0 + (uint32_t)lane < L.n ? L.G[j0 + lane] : 0ull, th, R, excl, idxmode, o, cum);
+        }
     } else {
         uint32_t b0 = 0;
         if (from > 0u) {
