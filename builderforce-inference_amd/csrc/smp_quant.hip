@@ -353,12 +353,26 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             const float vlo = fmaxf(vpre[q] * (1.0f - QEPS), vmx[q]);
             const float vhi = (vpre[q] + vsum[q]) * (1.0f + QEPS);
             const uint32_t velo = max(__float_as_uint(vlo) >> 23, 1u), vehi = max(__float_as_uint(vhi) >> 23, 1u);
-            uint32_t elo_e[EPV], wq = 0, zq = 0, vq = 0;
-            if (velo == vehi) {
+            uint32_t wq = 0, zq = 0, vq = 0;
+            // t + 2^23 rounds t to an integer (ties to even) in the low mantissa bits, for t
+            // below 2^23 (larger t is a window, whose units are not used)
+            if (velo == vehi) {  // one binade for the whole vector: only ties and large terms
+                const int32_t k = 150 - (int32_t)velo;
 #pragma unroll
-                for (int e = 0; e < EPV; e++) elo_e[e] = velo;
+                for (int e = 0; e < EPV; e++) {
+                    const float t = __builtin_ldexpf(ev[q][e], k);
+                    const float y = t + 8388608.0f;
+                    const float qf = y - 8388608.0f;
+                    // (a zero term gives t = 0: neither)
+                    wq |= ((fabsf(t - qf) == 0.5f) | !(t < 8388608.0f)) ? 1u << e : 0u;
+                    zq |= !(ev[q][e] > 0.0f) ? 1u << e : 0u;
+                    vq += __float_as_uint(y);
+                }
                 fbits |= 1u << q;
+#pragma unroll
+                for (int i = 0; i < EBW; i++) eb[q][i] = (velo & 0xFFu) * 0x01010101u;
             } else {
+                uint32_t elo_e[EPV];
                 float A = vpre[q], L = vmx[q];
 #pragma unroll
                 for (int e = 0; e < EPV; e++) {
@@ -372,25 +386,17 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                     A = An;
                     L = fmaxf(L, v);
                 }
-            }
 #pragma unroll
-            for (int e = 0; e < EPV; e++) {
-                const bool zero = !(ev[q][e] > 0.0f);
-                const float t = __builtin_ldexpf(ev[q][e], 150 - (int32_t)elo_e[e]);
-                // t + 2^23 rounds t to an integer (ties to even) in the low mantissa bits, for
-                // t below 2^23 (larger t is a window, whose units are not used)
-                const float y = t + 8388608.0f;
-                const float qf = y - 8388608.0f;
-                const bool win = !zero & (((wq >> e) & 1u) | (fabsf(t - qf) == 0.5f) | !(t < 8388608.0f));
-                zq |= zero ? 1u << e : 0u;
-                wq = win ? wq | (1u << e) : wq & ~(1u << e);
-                vq += __float_as_uint(y);
-            }
-            vqs[q] = vq - (uint32_t)EPV * 0x4B000000u;
-            if (velo == vehi) {
-#pragma unroll
-                for (int i = 0; i < EBW; i++) eb[q][i] = (velo & 0xFFu) * 0x01010101u;
-            } else {
+                for (int e = 0; e < EPV; e++) {
+                    const bool zero = !(ev[q][e] > 0.0f);
+                    const float t = __builtin_ldexpf(ev[q][e], 150 - (int32_t)elo_e[e]);
+                    const float y = t + 8388608.0f;
+                    const float qf = y - 8388608.0f;
+                    const bool win = !zero & (((wq >> e) & 1u) | (fabsf(t - qf) == 0.5f) | !(t < 8388608.0f));
+                    zq |= zero ? 1u << e : 0u;
+                    wq = win ? wq | (1u << e) : wq & ~(1u << e);
+                    vq += __float_as_uint(y);
+                }
 #pragma unroll
                 for (int i = 0; i < EBW; i++) {
                     uint32_t wd = 0;
@@ -399,6 +405,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                     eb[q][i] = wd;
                 }
             }
+            vqs[q] = vq - (uint32_t)EPV * 0x4B000000u;
             wmask |= wq << (q * EPV);
             zmask |= zq << (q * EPV);
         }
