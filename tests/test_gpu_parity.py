@@ -415,6 +415,50 @@ def test_extreme_magnitudes(smp):
     check(cfg, 256, smp)
 
 
+def _restreams(smp, cfg, cap):
+    """Per row: ranges the row kernel streamed exactly in a traced call (the phase trace keeps
+    the quantizing pass's workgroups' words (8 each), then 16 per row, word 9 that count)."""
+    import torch
+
+    d = workloads.to_device(cfg)
+    smp.set_tracing(True)
+    smp.target_rows(d["logits"], d["params"], d["u"], cap, d["hist"], d["hist_off"], d["mask"])
+    torch.cuda.synchronize()
+    smp.set_tracing(False)
+    tr = smp.trace().astype(np.int64)
+    B = cfg["B"]
+    nrc = (tr.size - B * 16) // 16
+    return tr[nrc * 8:nrc * 8 + B * 16].reshape(B, 16)[:, 9]
+
+
+def test_rows_whose_sum_outruns_the_prediction(smp):
+    """The reference's f32 normalizer drops every term below half a unit of its running sum.
+    Rows whose two large terms bring the sum just below 2, then ~150K terms each below half a
+    unit: the exact prefix the quantizing pass predicts from passes 2 while
+    the reference's sum stays below it, so the chain's binade checks fail (and chunks straddling
+    the boundary list more windows than they may) and the row kernel streams those chunks
+    exactly. The lost mass (~0.0087) exceeds the prediction's margin at 2 for the last chunks.
+    Tokens and kept sets must still be the reference's, and the exact streams must have run."""
+    rng = np.random.default_rng(17)
+    V = 151936
+    modes = [dict(temperature=1.0, top_p=0.9), dict(temperature=1.0), dict(temperature=1.0, min_p=0.3),
+             dict(temperature=1.0, top_k=3)]
+    rows, params = [], []
+    for k, m in enumerate(modes):
+        x = (-16.68 + rng.standard_normal(V) * 0.005).astype(np.float32)
+        x[0] = 0.0
+        x[1] = np.float32(np.log(0.996 - 0.0005 * k))
+        rows.append(x)
+        params.append(m)
+    # the premise: every small term is below half a unit of [1, 2), and the exact sum passes 2
+    e = np.exp(np.array(rows, np.float64))
+    assert e[:, 2:].max() < 2.0 ** -24 and (e.sum(1) > 2.0).all() and (e[:, :2].sum(1) < 2.0).all()
+    cfg = _cfg_from(rows, params, u=[0.2, 0.999, 0.5, 0.7])
+    cfg["name"] = "outrun"
+    check(cfg, 512, smp)
+    assert (_restreams(smp, cfg, 512) > 0).all()
+
+
 def test_c1_full_size_and_topk_over_many_chunks(smp):
     """B=1 at full vocabulary: 75 chunks each hand over their own top-k, so the list above
     the largest chunk bound holds thousands of entries and the select narrows it to about k."""
