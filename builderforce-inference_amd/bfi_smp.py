@@ -66,6 +66,8 @@ def lib():
         L.bfi_smp_verify.argtypes = [P, P, I32, I64, I64, I64, I64, P, P, P, P, P, P, I64, P, P, P, P, P]
         L.bfi_smp_sample_host.argtypes = [P, P, I64, P, I64, P, P, ctypes.c_float, P]
         L.bfi_smp_head.argtypes = [P, P, P, I32, ctypes.c_float, P, I64, I64, I64, P, P]
+        L.bfi_smp_dequant.argtypes = [P, I32, P, I64, P, P]
+        L.bfi_smp_head_typed.argtypes = [P, P, P, I32, ctypes.c_float, P, I32, I64, I64, I64, P, P]
         L.bfi_smp_head_sample_rows.argtypes = [P, P, P, I32, ctypes.c_float, P, I64, I64, I64, P, P, P, P, I64, P, P,
                                                P]
         L.bfi_rng_next_u64.argtypes = [P]
@@ -300,6 +302,32 @@ class Sampler:
         rc = self._L.bfi_smp_head(self._ctx, _dptr(x), _dptr(norm_w), 1 if norm_per_row else 0, ctypes.c_float(eps),
                                   _dptr(w), T, d, V, _dptr(out), self._stream(stream))
         self._check(rc, "bfi_smp_head")
+        return out
+
+    def dequant(self, ggml_type, src, n_weights, out=None, stream=None):
+        """A GGML tensor's weights (src: its bytes, a cuda uint8 tensor) to f32 on the device,
+        each value as the reference's dequant_row computes it; returns the flat f32 tensor."""
+        import torch
+
+        if out is None:
+            out = torch.empty(n_weights, dtype=torch.float32, device=src.device)
+        rc = self._L.bfi_smp_dequant(self._ctx, int(ggml_type), _dptr(src), int(n_weights), _dptr(out),
+                                     self._stream(stream))
+        self._check(rc, "bfi_smp_dequant")
+        return out
+
+    def head_typed(self, x, norm_w, eps, w, ggml_type, out=None, norm_per_row=False, stream=None):
+        """head over weights dequantized from GGML type ggml_type, in that type's dot order."""
+        import torch
+
+        T, d = x.shape
+        V = w.shape[0]
+        if out is None:
+            out = torch.empty((T, V), dtype=torch.float32, device=x.device)
+        rc = self._L.bfi_smp_head_typed(self._ctx, _dptr(x), _dptr(norm_w), 1 if norm_per_row else 0,
+                                        ctypes.c_float(eps), _dptr(w), int(ggml_type), T, d, V, _dptr(out),
+                                        self._stream(stream))
+        self._check(rc, "bfi_smp_head_typed")
         return out
 
     def head_sample_rows(self, x, norm_w, eps, w, params, u, out, hist=None, hist_off=None, mask=None,

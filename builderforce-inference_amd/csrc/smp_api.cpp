@@ -58,7 +58,8 @@ hipError_t launch_stream(const KArgs& a, int bf16, int vec, hipStream_t stream, 
 hipError_t launch_quant(const KArgs& a, int bf16, int vec, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 hipError_t launch_row(const KArgs& a, int bf16, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 hipError_t launch_head(const float* x, const float* norm_w, int norm_per_row, float eps, const float* W, int64_t n_tok,
-                       int64_t d, int64_t n_out, int vec, float* xn, float* out, hipStream_t stream);
+                       int64_t d, int64_t n_out, int vec, int blocked, float* xn, float* out, hipStream_t stream);
+hipError_t launch_dequant(int type, const void* src, int64_t n, float* dst, hipStream_t stream);
 }
 
 struct bfi_smp_ctx {
@@ -599,7 +600,7 @@ namespace {
 // The output head into `out` (n_tok x n_out f32), the normalized rows in the context's head
 // workspace (whose first `lead` bytes the caller may use too).
 int run_head(bfi_smp_ctx* ctx, const float* x, const float* norm_w, int norm_per_row, float eps, const float* W,
-             int64_t n_tok, int64_t d, int64_t n_out, float* out, size_t lead, hipStream_t stream) {
+             int64_t n_tok, int64_t d, int64_t n_out, float* out, size_t lead, hipStream_t stream, int blocked = 0) {
     if (!x || !norm_w || !W) return fail(ctx, BFI_SMP_EINVAL, "x, norm_w or W is NULL");
     if (n_tok < 0 || d <= 0 || n_out <= 0 || n_tok > (1 << 20) || n_out > ((int64_t)1 << 31) / 64)
         return fail(ctx, BFI_SMP_EINVAL, "head sizes out of range (n_tok %lld, d %lld, n_out %lld)", (long long)n_tok,
@@ -620,11 +621,51 @@ int run_head(bfi_smp_ctx* ctx, const float* x, const float* norm_w, int norm_per
     float* xn = (float*)(ctx->head + align_up(lead, 256));
     if (!out) out = (float*)ctx->head;
     const int vec = (d % 4 == 0) && ((uintptr_t)W % 16 == 0);
-    const hipError_t e = bfi::launch_head(x, norm_w, norm_per_row, eps, W, n_tok, d, n_out, vec, xn, out, stream);
+    const hipError_t e = bfi::launch_head(x, norm_w, norm_per_row, eps, W, n_tok, d, n_out, vec, blocked, xn, out, stream);
     return e == hipSuccess ? BFI_SMP_OK : hip_fail(ctx, e, "head launch");
 }
 
+// Weights a block of each GGML type this head takes holds (0: a type it does not take).
+int64_t ggml_block_elems(int32_t type) {
+    switch (type) {
+        case 0: case 1: case 30: return 1;  // F32, F16, BF16
+        case 2: case 8: return 32;           // Q4_0, Q8_0
+        case 14: return 256;                 // Q6_K
+        default: return 0;
+    }
+}
+
 }  // namespace
+
+int bfi_smp_dequant(bfi_smp_ctx* ctx, int32_t ggml_type, const void* d_src, int64_t n_weights, float* d_dst,
+                    void* stream) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    const int64_t be = ggml_block_elems(ggml_type);
+    if (be == 0 || ggml_type == 0)
+        return fail(ctx, BFI_SMP_EINVAL, "GGML type %d is not one this head dequantizes", (int)ggml_type);
+    if (n_weights < 0 || n_weights % be != 0)
+        return fail(ctx, BFI_SMP_EINVAL, "%lld weights is not a whole number of %lld-weight blocks",
+                    (long long)n_weights, (long long)be);
+    if (n_weights > 0 && (!d_src || !d_dst)) return fail(ctx, BFI_SMP_EINVAL, "d_src or d_dst is NULL");
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+    const hipError_t e = bfi::launch_dequant(ggml_type, d_src, n_weights, d_dst, (hipStream_t)stream);
+    return e == hipSuccess ? BFI_SMP_OK : hip_fail(ctx, e, "dequant launch");
+}
+
+int bfi_smp_head_typed(bfi_smp_ctx* ctx, const float* d_x, const float* d_norm_w, int norm_per_row, float eps,
+                       const float* d_w, int32_t ggml_type, int64_t n_tokens, int64_t n_embd, int64_t n_vocab,
+                       float* d_logits, void* stream) {
+    if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    if (!d_logits) return fail(ctx, BFI_SMP_EINVAL, "d_logits is NULL");
+    if (ggml_block_elems(ggml_type) == 0)
+        return fail(ctx, BFI_SMP_EINVAL, "GGML type %d is not one this head takes", (int)ggml_type);
+    // cpu.rs:515-563: the types with a fused block dot (Q8_0, Q4_0) sum by blocks when the row
+    // is whole blocks; every other type, and a row of partial blocks, is one dot over the row
+    const int blocked = (ggml_type == 8 || ggml_type == 2) && n_embd % 32 == 0;
+    return run_head(ctx, d_x, d_norm_w, norm_per_row, eps, d_w, n_tokens, n_embd, n_vocab, d_logits, 0,
+                    (hipStream_t)stream, blocked);
+}
 
 int bfi_smp_head(bfi_smp_ctx* ctx, const float* d_x, const float* d_norm_w, int norm_per_row, float eps,
                  const float* d_w, int64_t n_tokens, int64_t n_embd, int64_t n_vocab, float* d_logits, void* stream) {

@@ -55,6 +55,49 @@ __global__ __launch_bounds__(HN_BLOCK) void k_head_norm(const float* __restrict_
     for (int64_t i = threadIdx.x; i < d; i += HN_BLOCK) out[r * d + i] = xr[i] * scale * wr[i];
 }
 
+// ---- weight formats (GGML type ids, crates/bfi-gguf/src/types/mod.rs:35-42) ------------------
+// Every weight dequantized exactly as the reference's dequant_row computes it (types/*.rs):
+// F16 and BF16 widen exactly; Q8_0 is q * d, Q4_0 (nibble - 8) * d, Q6_K (d * scale) * q, each
+// product one f32 rounding, d an f16 widened exactly. One thread per weight.
+constexpr int GT_F16 = 1, GT_Q4_0 = 2, GT_Q8_0 = 8, GT_Q6_K = 14, GT_BF16 = 30;
+
+__device__ __forceinline__ float f16_at(const uint8_t* p) {
+    const uint16_t h = (uint16_t)p[0] | ((uint16_t)p[1] << 8);
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src, int64_t n, float* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v;
+    if (TYPE == GT_F16) {
+        v = f16_at(src + 2 * i);
+    } else if (TYPE == GT_BF16) {
+        const uint32_t h = (uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 8);
+        v = __uint_as_float(h << 16);
+    } else if (TYPE == GT_Q8_0) {  // q8_0.rs:4-9: 34-byte blocks of 32
+        const uint8_t* b = src + (i / 32) * 34;
+        v = (float)(int8_t)b[2 + i % 32] * f16_at(b);
+    } else if (TYPE == GT_Q4_0) {  // q4_0.rs:4-12: 18-byte blocks of 32, low nibbles first
+        const uint8_t* b = src + (i / 32) * 18;
+        const int k = (int)(i % 32);
+        const uint8_t byte = b[2 + (k & 15)];
+        const int nib = k < 16 ? (byte & 0x0F) : (byte >> 4);
+        v = ((float)nib - 8.0f) * f16_at(b);
+    } else {  // GT_Q6_K, q6_k.rs:4-29: 210-byte blocks of 256 (ql[128], qh[64], scales[16], d)
+        const uint8_t* b = src + (i / 256) * 210;
+        const int k = (int)(i % 256), nh = k / 128, quarter = (k % 128) / 32, l = k % 32;
+        const uint8_t* ql = b + nh * 64;
+        const uint8_t qh = b[128 + nh * 32 + l];
+        const uint8_t lo = ql[l + ((quarter & 1) ? 32 : 0)];
+        const int q = ((quarter < 2 ? (lo & 0x0F) : (lo >> 4)) | (((qh >> (2 * quarter)) & 3) << 4)) - 32;
+        const float sc = (float)(int8_t)b[192 + nh * 8 + l / 16 + 2 * quarter];
+        v = (f16_at(b + 208) * sc) * (float)q;
+    }
+    dst[i] = v;
+}
+
 constexpr int HG_BO = 64;   // outputs (rows of W) a block
 constexpr int HG_BT = 64;   // tokens a block
 constexpr int HG_K = 16;    // inner-dimension chunk staged through LDS
@@ -62,7 +105,10 @@ constexpr int HG_BLOCK = 256;
 
 // out[t][o] = sum over i in index order of W[o][i] * X[t][i]. A thread owns 4 outputs x 4
 // tokens; each chunk of 16 inner positions is staged transposed in LDS so a thread reads
-// its 4 weights and 4 inputs of one position as two 16-byte loads.
+// its 4 weights and 4 inputs of one position as two 16-byte loads. BLOCKED: the fused block
+// dot of the Q8_0 and Q4_0 formats (q8_0.rs:11-15, cpu.rs:550-563): each 32-weight block's
+// products summed from -0.0, the block sums added from +0.0 (d a multiple of 32).
+template <bool BLOCKED>
 __global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict__ W, const float* __restrict__ X,
                                                         int64_t n_out, int64_t n_tok, int64_t d, int vec,
                                                         float* __restrict__ out) {
@@ -71,11 +117,14 @@ __global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict_
     const int tid = threadIdx.x;
     const int to = tid % 16, tt = tid / 16;  // this thread: outputs 4 to.., tokens 4 tt..
     const int64_t o0 = (int64_t)blockIdx.x * HG_BO, t0 = (int64_t)blockIdx.y * HG_BT;
-    float acc[4][4];
+    float acc[4][4], part[4][4];  // (part: the current block's sum, BLOCKED)
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) acc[a][b] = -0.0f;
+        for (int b = 0; b < 4; b++) {
+            acc[a][b] = BLOCKED ? 0.0f : -0.0f;
+            part[a][b] = -0.0f;
+        }
     // staging: thread tid loads 4 consecutive inner positions of one row of the tile
     const int lr = tid / 4, lc = (tid % 4) * 4;
     const int64_t wrow = o0 + lr, xrow = t0 + lr;
@@ -108,7 +157,19 @@ __global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict_
 #pragma unroll
             for (int p = 0; p < 4; p++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) acc[p][q] = acc[p][q] + av[p] * bv[q];
+                for (int q = 0; q < 4; q++) {
+                    if (BLOCKED) part[p][q] = part[p][q] + av[p] * bv[q];
+                    else acc[p][q] = acc[p][q] + av[p] * bv[q];
+                }
+        }
+        if (BLOCKED && ((k0 + HG_K) % 32) == 0) {  // (a block ends with every other chunk)
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    acc[p][q] = acc[p][q] + part[p][q];
+                    part[p][q] = -0.0f;
+                }
         }
     }
 #pragma unroll
@@ -127,12 +188,32 @@ __global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict_
 
 // xn: n_tok * d floats of workspace; out: n_tok * n_out logits.
 // vec: d % 4 == 0 and W 16-byte aligned (the rows then load as 16-byte vectors).
+// blocked: the Q8_0 / Q4_0 block dot order (d % 32 == 0).
 hipError_t launch_head(const float* x, const float* norm_w, int norm_per_row, float eps, const float* W,
-                       int64_t n_tok, int64_t d, int64_t n_out, int vec, float* xn, float* out, hipStream_t stream) {
+                       int64_t n_tok, int64_t d, int64_t n_out, int vec, int blocked, float* xn, float* out,
+                       hipStream_t stream) {
     if (n_tok <= 0 || n_out <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_head_norm, dim3((unsigned)n_tok), dim3(HN_BLOCK), 0, stream, x, norm_w, norm_per_row, eps, d, xn);
     const dim3 grid((unsigned)((n_out + HG_BO - 1) / HG_BO), (unsigned)((n_tok + HG_BT - 1) / HG_BT));
-    hipLaunchKernelGGL(k_head_gemm, grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out);
+    if (blocked) hipLaunchKernelGGL(k_head_gemm<true>, grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out);
+    else hipLaunchKernelGGL(k_head_gemm<false>, grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out);
+    return hipGetLastError();
+}
+
+// n weights of a GGML tensor (n a multiple of the type's block) to f32; hipErrorInvalidValue
+// for a type this head does not take.
+hipError_t launch_dequant(int type, const void* src, int64_t n, float* dst, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    const uint8_t* s = static_cast<const uint8_t*>(src);
+    switch (type) {
+        case GT_F16: hipLaunchKernelGGL(k_dequant<GT_F16>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_BF16: hipLaunchKernelGGL(k_dequant<GT_BF16>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_Q8_0: hipLaunchKernelGGL(k_dequant<GT_Q8_0>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_Q4_0: hipLaunchKernelGGL(k_dequant<GT_Q4_0>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_Q6_K: hipLaunchKernelGGL(k_dequant<GT_Q6_K>, grid, dim3(256), 0, stream, s, n, dst); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -205,8 +205,8 @@ int bfi_smp_sample_host(bfi_smp_ctx *ctx, const float *logits, int64_t n_vocab,
  * n_vocab] f32. Rounding as the CPU backend's (cpu.rs:92-120, 498-514): the mean of squares
  * and every dot product summed one f32 addition at a time in index order (from -0.0, Rust's
  * f32 `Sum`), sqrt and 1/x correctly rounded, x * scale * w left to right; the logits are
- * bit-identical to the reference's. Quantized lm_head weights (matmul_quant,
- * cpu.rs:516-545) are not taken. Asynchronous on `stream`; n_tokens <= 2^20.
+ * bit-identical to the reference's. Quantized lm_head weights: bfi_smp_dequant, then
+ * bfi_smp_head_typed. Asynchronous on `stream`; n_tokens <= 2^20.
  */
 int bfi_smp_head(bfi_smp_ctx *ctx, const float *d_x, const float *d_norm_w, int norm_per_row,
                  float eps, const float *d_w, int64_t n_tokens, int64_t n_embd, int64_t n_vocab,
@@ -223,6 +223,29 @@ int bfi_smp_head_sample_rows(bfi_smp_ctx *ctx, const float *d_x, const float *d_
                              const uint32_t *d_hist, const int64_t *d_hist_off,
                              const uint32_t *d_mask, int64_t mask_stride, const float *d_u,
                              uint32_t *d_out, void *stream);
+
+/*
+ * Dequantizes n_weights weights of a GGML tensor (d_src: its bytes on the device, rows of
+ * whole blocks) to f32 in d_dst, every value exactly as the reference's dequant_row computes
+ * it (crates/bfi-gguf/src/types/, one file a format; replaces `dequant_tensor`, types/mod.rs, as
+ * `matmul_quant` uses it, crates/bfi-core/src/cpu.rs:515-563): ggml_type 1 (F16), 30 (BF16),
+ * 8 (Q8_0: q * d), 2 (Q4_0: (nibble - 8) * d), 14 (Q6_K: (d * scale) * q). A model's lm_head is
+ * dequantized once, at load. BFI_SMP_EINVAL for another type or a partial block.
+ */
+int bfi_smp_dequant(bfi_smp_ctx *ctx, int32_t ggml_type, const void *d_src, int64_t n_weights,
+                    float *d_dst, void *stream);
+
+/*
+ * bfi_smp_head over lm_head weights dequantized from GGML type ggml_type (d_w: bfi_smp_dequant's
+ * output; 0 for f32 weights), in the dot order `matmul_quant` uses for that type
+ * (cpu.rs:515-563): Q8_0 and Q4_0 have a fused block dot (q8_0.rs:11-15, q4_0.rs:14-18) — each
+ * 32-weight block's products summed from -0.0, the block sums added from +0.0 — when n_embd is
+ * a multiple of 32; F16, BF16, Q6_K (no block dot) and rows of partial blocks take one dot over
+ * the row, as f32 weights do. Logits bit-identical to the reference's for that tensor.
+ */
+int bfi_smp_head_typed(bfi_smp_ctx *ctx, const float *d_x, const float *d_norm_w, int norm_per_row,
+                       float eps, const float *d_w, int32_t ggml_type, int64_t n_tokens,
+                       int64_t n_embd, int64_t n_vocab, float *d_logits, void *stream);
 
 /* ---- host-side helpers (no GPU work) ------------------------------------ */
 

@@ -701,3 +701,95 @@ void orc_matmul_f32(const float *w, const float *x, int64_t n_tokens, int64_t n_
             out[t * n_out + o] = s;
         }
 }
+
+/* ---- lm_head weight formats (crates/bfi-gguf/src/types/, one file a format) ---------------- */
+
+/* IEEE binary16 widened to binary32 (f16.rs:4-6, the `half` crate's exact conversion). */
+static float orc_f16(const uint8_t *p) {
+    const uint16_t h = (uint16_t)(p[0] | (p[1] << 8));
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, ex = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+    float v;
+    if (ex == 0) {
+        v = ldexpf((float)man, -24); /* subnormal (or zero): man * 2^-24, exact */
+        uint32_t b;
+        memcpy(&b, &v, 4);
+        b |= sign;
+        memcpy(&v, &b, 4);
+        return v;
+    }
+    uint32_t b = ex == 31 ? (sign | 0x7F800000u | (man << 13)) : (sign | ((ex - 15u + 127u) << 23) | (man << 13));
+    memcpy(&v, &b, 4);
+    return v;
+}
+
+/* dequant_row of each type, for n weights (whole blocks): f16.rs, bf16.rs, q8_0.rs:4-9,
+ * q4_0.rs:4-12, q6_k.rs:4-29. Returns 0, or -1 for a type not restated. */
+int orc_dequant(int type, const uint8_t *src, int64_t n, float *dst) {
+    for (int64_t i = 0; i < n; i++) {
+        float v;
+        if (type == 1) {
+            v = orc_f16(src + 2 * i);
+        } else if (type == 30) {
+            const uint32_t b = ((uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 8)) << 16;
+            memcpy(&v, &b, 4);
+        } else if (type == 8) {
+            const uint8_t *blk = src + (i / 32) * 34;
+            const float d = orc_f16(blk);
+            v = (float)(int8_t)blk[2 + i % 32] * d;
+        } else if (type == 2) {
+            const uint8_t *blk = src + (i / 32) * 18;
+            const float d = orc_f16(blk);
+            const int64_t j = i % 32;
+            const uint8_t byte = blk[2 + (j % 16)];
+            v = ((float)(j < 16 ? (byte & 0x0F) : (byte >> 4)) - 8.0f) * d;
+        } else if (type == 14) {
+            const uint8_t *blk = src + (i / 256) * 210;
+            const int64_t k = i % 256, half = k / 128, r = k % 128, l = r % 32;
+            const uint8_t *ql = blk + half * 64, *qh = blk + 128 + half * 32, *sc = blk + 192 + half * 8;
+            const float d = orc_f16(blk + 208);
+            int q;
+            float s;
+            if (r < 32) {
+                q = ((ql[l] & 0x0F) | ((qh[l] & 3) << 4)) - 32;
+                s = (float)(int8_t)sc[l / 16];
+            } else if (r < 64) {
+                q = ((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                s = (float)(int8_t)sc[l / 16 + 2];
+            } else if (r < 96) {
+                q = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                s = (float)(int8_t)sc[l / 16 + 4];
+            } else {
+                q = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                s = (float)(int8_t)sc[l / 16 + 6];
+            }
+            v = d * s * (float)q;
+        } else {
+            return -1;
+        }
+        dst[i] = v;
+    }
+    return 0;
+}
+
+/* matmul_quant's dot order for a type with a fused block dot (cpu.rs:550-563 with
+ * q8_0.rs:11-15 / q4_0.rs:14-18): per block of `block` weights the products summed from -0.0,
+ * the block sums added from +0.0; w holds the dequantized weights. block 0: one dot over the
+ * row (orc_matmul_f32's order). */
+void orc_matmul_blocked(const float *w, const float *x, int64_t n_tokens, int64_t n_out, int64_t n_in,
+                        int64_t block, float *out) {
+    if (block <= 0) {
+        orc_matmul_f32(w, x, n_tokens, n_out, n_in, out);
+        return;
+    }
+    for (int64_t t = 0; t < n_tokens; t++)
+        for (int64_t o = 0; o < n_out; o++) {
+            const float *wr = w + o * n_in, *xr = x + t * n_in;
+            float s = 0.0f;
+            for (int64_t b = 0; b < n_in; b += block) {
+                float p = -0.0f;
+                for (int64_t i = b; i < b + block && i < n_in; i++) p = p + wr[i] * xr[i];
+                s = s + p;
+            }
+            out[t * n_out + o] = s;
+        }
+}

@@ -31,6 +31,13 @@
  *   orc_rms_norm, orc_matmul_f32   reference KATs rms_norm_ones / matmul_f32_identity
  *                                  (cpu.rs:835-855) + numpy's sequential float32 accumulate
  *                                  and correctly rounded sqrt on random rows
+ *   orc_dequant                    F16: all 65,536 codes against numpy's float16; BF16: against
+ *                                  torch's bfloat16; Q8_0 / Q4_0 / Q6_K: the reference's KATs
+ *                                  (q8_0.rs, q4_0.rs, q6_k.rs, types/mod.rs:300-328) and layouts
+ *                                  with known small-integer values at every nibble, high-bit
+ *                                  pair and scale position
+ *   orc_matmul_blocked             a closed form where block sums keep what one row sum loses
+ *                                  (2^24 then 63 ones: 2^24 + 32 against 2^24)
  */
 #ifndef BFI_ORACLE_H
 #define BFI_ORACLE_H
@@ -109,6 +116,9 @@ void orc_rms_norm(const float *x, const float *w, int w_per_row, float eps, int6
                   float *out);
 void orc_matmul_f32(const float *w, const float *x, int64_t n_tokens, int64_t n_out, int64_t n_in,
                     float *out);
+int orc_dequant(int type, const uint8_t *src, int64_t n, float *dst);
+void orc_matmul_blocked(const float *w, const float *x, int64_t n_tokens, int64_t n_out, int64_t n_in,
+                        int64_t block, float *out);
 
 #ifdef __cplusplus
 }

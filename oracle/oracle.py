@@ -127,6 +127,10 @@ def lib(path=None):
         L.orc_rms_norm.restype = None
         L.orc_matmul_f32.argtypes = [P, P, I64, I64, I64, P]
         L.orc_matmul_f32.restype = None
+        L.orc_dequant.argtypes = [ctypes.c_int, P, I64, P]
+        L.orc_dequant.restype = ctypes.c_int
+        L.orc_matmul_blocked.argtypes = [P, P, I64, I64, I64, I64, P]
+        L.orc_matmul_blocked.restype = None
         L.orc_verify_seq.argtypes = [
             P, ctypes.c_int, I64, I64, P, P, ctypes.c_size_t, P, ctypes.c_size_t, P, I64, P,
             ctypes.c_float, P, P,
@@ -151,6 +155,25 @@ def matmul_f32(w, x):
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty((x.shape[0], w.shape[0]), np.float32)
     lib().orc_matmul_f32(_ptr(w), _ptr(x), x.shape[0], w.shape[0], w.shape[1], _ptr(out))
+    return out
+
+
+def dequant(ggml_type: int, src, n: int):
+    """A GGML tensor's first n weights (src: its bytes) to float32 (types/<format>.rs)."""
+    src = np.ascontiguousarray(src, np.uint8)
+    out = np.empty(n, np.float32)
+    if lib().orc_dequant(int(ggml_type), _ptr(src), n, _ptr(out)) != 0:
+        raise ValueError(f"GGML type {ggml_type} is not restated")
+    return out
+
+
+def matmul_blocked(w, x, block: int):
+    """matmul_quant's dot order (cpu.rs:550-563) over dequantized weights: blocks of `block`
+    products summed from -0.0, the blocks from +0.0 (block 0: one dot over the row)."""
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty((x.shape[0], w.shape[0]), np.float32)
+    lib().orc_matmul_blocked(_ptr(w), _ptr(x), x.shape[0], w.shape[0], w.shape[1], int(block), _ptr(out))
     return out
 
 

@@ -88,3 +88,73 @@ def test_qwen3_sized_head_and_fused_sampling(smp):
     torch.cuda.synchronize()
     want = O.sample_rows(logits, params, hist, off, u)
     assert out.cpu().numpy().astype(np.uint32).tolist() == [int(t) for t in want]
+
+
+# ---- quantized lm_head weights (bfi_smp_dequant, bfi_smp_head_typed) ---------------------------
+
+BLOCK = {1: (1, 2), 30: (1, 2), 8: (32, 34), 2: (32, 18), 14: (256, 210)}
+
+
+def _random_tensor(rng, ggml_type, n):
+    """Random bytes of a GGML tensor of n weights with finite f16 scales."""
+    be, bb = BLOCK[ggml_type]
+    nb = n // be
+    raw = rng.integers(0, 256, nb * bb, dtype=np.uint8).reshape(nb, bb)
+    if ggml_type == 1:  # finite f16 weights
+        raw = (rng.standard_normal(n) * 0.1).astype(np.float16).view(np.uint8).reshape(nb, bb)
+    elif ggml_type == 30:  # finite bf16 weights (the top halves of f32 values)
+        top = ((rng.standard_normal(n) * 0.1).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        raw = top.view(np.uint8).reshape(nb, bb)
+    elif ggml_type in (8, 2):
+        raw[:, 0:2] = (rng.standard_normal(nb) * 0.01).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif ggml_type == 14:
+        raw[:, 208:210] = (rng.standard_normal(nb) * 0.001).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("ggml_type", [1, 30, 8, 2, 14])
+def test_device_dequant_matches_oracle(smp, ggml_type):
+    import torch
+
+    rng = np.random.default_rng(ggml_type)
+    n = 256 * 97
+    src = _random_tensor(rng, ggml_type, n)
+    got = smp.dequant(ggml_type, _dev(src), n)
+    torch.cuda.synchronize()
+    want = O.dequant(ggml_type, src, n)
+    g = got.cpu().numpy()
+    fin = np.isfinite(want)
+    assert np.array_equal(g[fin].view(np.uint32), want[fin].view(np.uint32))
+    assert (np.isnan(g) == np.isnan(want)).all()
+
+
+@pytest.mark.parametrize("ggml_type,d", [(8, 256), (8, 1000), (2, 64), (14, 256), (1, 130), (30, 64)])
+def test_typed_head_matches_oracle_bitwise(smp, ggml_type, d):
+    """Q8_0 and Q4_0 rows of whole blocks take the block dot order, other rows one dot."""
+    import torch
+
+    rng = np.random.default_rng(ggml_type * 7 + d)
+    T, V = 9, 1028
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    nw = rng.standard_normal(d).astype(np.float32)
+    src = _random_tensor(rng, ggml_type, V * d)
+    w_dev = smp.dequant(ggml_type, _dev(src), V * d).view(V, d)
+    out = smp.head_typed(_dev(x), _dev(nw), 1e-6, w_dev, ggml_type)
+    torch.cuda.synchronize()
+    w = O.dequant(ggml_type, src, V * d).reshape(V, d)
+    xn = O.rms_norm(x, nw, 1e-6)
+    block = 32 if ggml_type in (8, 2) and d % 32 == 0 else 0
+    want = O.matmul_blocked(w, xn, block)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    if block:  # the order matters at this size: the one-dot order differs somewhere
+        assert not np.array_equal(O.matmul_f32(w, xn).view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_rejects_partial_blocks_and_other_types(smp):
+    import torch
+
+    src = torch.zeros(64, dtype=torch.uint8, device="cuda:0")
+    with pytest.raises(bfi_smp.SamplerError):
+        smp.dequant(8, src, 31)
+    with pytest.raises(bfi_smp.SamplerError):
+        smp.dequant(12, src, 256)  # Q4_K: not taken

@@ -58,3 +58,90 @@ def test_rms_norm_matches_numpy_statement():
     w2 = rng.standard_normal((2, 8)).astype(np.float32)
     got = O.rms_norm(x, w2, 1e-5, w_per_row=True)
     assert np.array_equal(got[1], O.rms_norm(x[1:], w2[1], 1e-5)[0])
+
+
+# ---- lm_head weight formats (orc_dequant, orc_matmul_blocked) ----------------------------------
+
+
+def _f16_bytes(v):
+    return np.frombuffer(np.float16(v).tobytes(), np.uint8)
+
+
+def test_dequant_f16_every_code_and_bf16_against_torch():
+    codes = np.arange(65536, dtype=np.uint16)
+    got = O.dequant(1, codes.view(np.uint8), 65536).view(np.uint32)
+    want = codes.view(np.float16).astype(np.float32).view(np.uint32)
+    assert np.array_equal(got, want)
+    import torch
+
+    rng = np.random.default_rng(5)
+    bits = rng.integers(0, 65536, 4096, dtype=np.uint16)
+    got = O.dequant(30, bits.view(np.uint8), bits.size)
+    want = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).float().numpy()
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    assert (np.isnan(got) == np.isnan(want)).all()
+
+
+def test_dequant_reference_kats():
+    # q8_0.rs:21-31 and types/mod.rs:310-317: d = 1, qs[0] = 5, qs[1] = -3
+    b = np.zeros(34, np.uint8)
+    b[0:2] = _f16_bytes(1.0)
+    b[2], b[3] = 5, np.uint8(256 - 3)
+    out = O.dequant(8, b, 32)
+    assert out[0] == 5.0 and out[1] == -3.0 and (out[2:] == 0).all()
+    # q4_0.rs:24-32: d = 1, every nibble 0 -> -8
+    b = np.zeros(18, np.uint8)
+    b[0:2] = _f16_bytes(1.0)
+    assert (O.dequant(2, b, 32) == -8.0).all()
+    # q6_k.rs:36-41, types/mod.rs:324-327: an all-zero block (d = 0) is all zeros
+    assert (O.dequant(14, np.zeros(210, np.uint8), 256) == 0.0).all()
+
+
+def test_dequant_layouts_place_every_weight():
+    """Blocks built by an encoder (the inverse of each layout) from known small-integer values:
+    a wrong nibble, high-bit pair or scale index moves a value and fails."""
+    # Q8_0: d = 0.5, q_i = i - 16
+    b = np.zeros(34, np.uint8)
+    b[0:2] = _f16_bytes(0.5)
+    b[2:] = (np.arange(32) - 16).astype(np.int8).view(np.uint8)
+    assert O.dequant(8, b, 32).tolist() == [(i - 16) * 0.5 for i in range(32)]
+    # Q4_0: d = 2, weight j < 16 in the low nibble of byte j, weight j + 16 in its high nibble
+    nib = np.arange(32) % 16
+    nib[16:] = 15 - nib[16:]
+    b = np.zeros(18, np.uint8)
+    b[0:2] = _f16_bytes(2.0)
+    b[2:] = (nib[:16] | (nib[16:] << 4)).astype(np.uint8)
+    assert O.dequant(2, b, 32).tolist() == [float((v - 8) * 2) for v in nib]
+    # Q6_K: d = 0.25, sixteen scales 1..16 (scale i covers weights 16 i .. 16 i + 15), and
+    # q = (k * 7) % 64 - 32 at weight k, encoded into ql / qh
+    q = (np.arange(256) * 7) % 64
+    sc = np.arange(1, 17, dtype=np.int8)
+    blk = np.zeros(210, np.uint8)
+    for k in range(256):
+        half, r = divmod(k, 128)
+        quarter, l = divmod(r, 32)
+        v = int(q[k])
+        qi = half * 64 + l + (32 if quarter in (1, 3) else 0)
+        blk[qi] |= (v & 15) << (4 if quarter >= 2 else 0)
+        blk[128 + half * 32 + l] |= (v >> 4) << (2 * quarter)
+    blk[192:208] = sc.view(np.uint8)
+    blk[208:210] = _f16_bytes(0.25)
+    # the scale of weight k: sixteen weights a scale, in the order the quarters are stored
+    want = []
+    for k in range(256):
+        half, r = divmod(k, 128)
+        quarter, l = divmod(r, 32)
+        s = int(sc[half * 8 + l // 16 + 2 * quarter])
+        want.append(0.25 * s * (int(q[k]) - 32))
+    assert O.dequant(14, blk, 256).tolist() == want
+
+
+def test_blocked_dot_keeps_what_one_row_sum_loses():
+    w = np.array([[2.0 ** 24] + [1.0] * 63], np.float32)
+    x = np.ones((1, 64), np.float32)
+    assert O.matmul_blocked(w, x, 32)[0, 0] == 2.0 ** 24 + 32
+    assert O.matmul_blocked(w, x, 0)[0, 0] == 2.0 ** 24
+    # a partial last block sums what it holds
+    w2 = np.array([[1.0] * 40], np.float32)
+    assert O.matmul_blocked(w2, np.ones((1, 40), np.float32), 32)[0, 0] == 40.0
