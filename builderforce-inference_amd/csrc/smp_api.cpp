@@ -630,7 +630,7 @@ int64_t ggml_block_elems(int32_t type) {
     switch (type) {
         case 0: case 1: case 30: return 1;  // F32, F16, BF16
         case 2: case 8: return 32;           // Q4_0, Q8_0
-        case 14: return 256;                 // Q6_K
+        case 12: case 13: case 14: return 256;  // Q4_K, Q5_K, Q6_K
         default: return 0;
     }
 }

@@ -57,9 +57,21 @@ __global__ __launch_bounds__(HN_BLOCK) void k_head_norm(const float* __restrict_
 
 // ---- weight formats (GGML type ids, crates/bfi-gguf/src/types/mod.rs:35-42) ------------------
 // Every weight dequantized exactly as the reference's dequant_row computes it (types/*.rs):
-// F16 and BF16 widen exactly; Q8_0 is q * d, Q4_0 (nibble - 8) * d, Q6_K (d * scale) * q, each
-// product one f32 rounding, d an f16 widened exactly. One thread per weight.
-constexpr int GT_F16 = 1, GT_Q4_0 = 2, GT_Q8_0 = 8, GT_Q6_K = 14, GT_BF16 = 30;
+// F16 and BF16 widen exactly; Q8_0 is q * d, Q4_0 (nibble - 8) * d, Q6_K (d * scale) * q, Q4_K
+// and Q5_K (d * scale) * q - dmin * min, each product and difference one f32 rounding, d an
+// f16 widened exactly. One thread per weight.
+constexpr int GT_F16 = 1, GT_Q4_0 = 2, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q5_K = 13, GT_Q6_K = 14, GT_BF16 = 30;
+
+// The 6-bit scale and min of sub-block j of a K-quant block (k_scale.rs:3-11).
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint32_t& sc, uint32_t& m) {
+    if (j < 4) {
+        sc = q[j] & 63u;
+        m = q[j + 4] & 63u;
+    } else {
+        sc = (q[j + 4] & 0x0Fu) | ((uint32_t)(q[j - 4] >> 6) << 4);
+        m = (uint32_t)(q[j + 4] >> 4) | ((uint32_t)(q[j] >> 6) << 4);
+    }
+}
 
 __device__ __forceinline__ float f16_at(const uint8_t* p) {
     const uint16_t h = (uint16_t)p[0] | ((uint16_t)p[1] << 8);
@@ -85,6 +97,19 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src
         const uint8_t byte = b[2 + (k & 15)];
         const int nib = k < 16 ? (byte & 0x0F) : (byte >> 4);
         v = ((float)nib - 8.0f) * f16_at(b);
+    } else if (TYPE == GT_Q4_K || TYPE == GT_Q5_K) {
+        // q4_k.rs:6-29 (144-byte blocks: d, dmin, 12 scale bytes, 128 qs) and q5_k.rs:6-36
+        // (176 bytes: the same, then qh[32] before 128 qs): (d * sc) * q - dmin * m, q a nibble
+        // (Q5_K: plus 16 for its high bit)
+        const int BB = TYPE == GT_Q4_K ? 144 : 176;
+        const uint8_t* b = src + (i / 256) * BB;
+        const int k = (int)(i % 256), group = k / 64, hi = (k % 64) / 32, l = k % 32;
+        uint32_t sc, m;
+        scale_min_k4(2 * group + hi, b + 4, sc, m);
+        const uint8_t byte = b[(TYPE == GT_Q4_K ? 16 : 48) + group * 32 + l];
+        float qv = (float)(hi ? (byte >> 4) : (byte & 0x0F));
+        if (TYPE == GT_Q5_K) qv = qv + (((b[16 + l] >> (2 * group + hi)) & 1u) ? 16.0f : 0.0f);
+        v = (f16_at(b) * (float)sc) * qv - f16_at(b + 2) * (float)m;
     } else {  // GT_Q6_K, q6_k.rs:4-29: 210-byte blocks of 256 (ql[128], qh[64], scales[16], d)
         const uint8_t* b = src + (i / 256) * 210;
         const int k = (int)(i % 256), nh = k / 128, quarter = (k % 128) / 32, l = k % 32;
@@ -212,6 +237,8 @@ hipError_t launch_dequant(int type, const void* src, int64_t n, float* dst, hipS
         case GT_Q8_0: hipLaunchKernelGGL(k_dequant<GT_Q8_0>, grid, dim3(256), 0, stream, s, n, dst); break;
         case GT_Q4_0: hipLaunchKernelGGL(k_dequant<GT_Q4_0>, grid, dim3(256), 0, stream, s, n, dst); break;
         case GT_Q6_K: hipLaunchKernelGGL(k_dequant<GT_Q6_K>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_Q4_K: hipLaunchKernelGGL(k_dequant<GT_Q4_K>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_Q5_K: hipLaunchKernelGGL(k_dequant<GT_Q5_K>, grid, dim3(256), 0, stream, s, n, dst); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

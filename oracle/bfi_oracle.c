@@ -723,7 +723,8 @@ static float orc_f16(const uint8_t *p) {
 }
 
 /* dequant_row of each type, for n weights (whole blocks): f16.rs, bf16.rs, q8_0.rs:4-9,
- * q4_0.rs:4-12, q6_k.rs:4-29. Returns 0, or -1 for a type not restated. */
+ * q4_0.rs:4-12, q4_k.rs:6-29, q5_k.rs:6-36, q6_k.rs:4-29. Returns 0, or -1 for a type not
+ * restated. */
 int orc_dequant(int type, const uint8_t *src, int64_t n, float *dst) {
     for (int64_t i = 0; i < n; i++) {
         float v;
@@ -742,6 +743,27 @@ int orc_dequant(int type, const uint8_t *src, int64_t n, float *dst) {
             const int64_t j = i % 32;
             const uint8_t byte = blk[2 + (j % 16)];
             v = ((float)(j < 16 ? (byte & 0x0F) : (byte >> 4)) - 8.0f) * d;
+        } else if (type == 12 || type == 13) {
+            /* q4_k.rs:6-29, q5_k.rs:6-36, k_scale.rs:3-11 */
+            const int bb = type == 12 ? 144 : 176;
+            const uint8_t *blk = src + (i / 256) * bb, *scl = blk + 4;
+            const int64_t k = i % 256, group = k / 64, hi = (k % 64) / 32, l = k % 32;
+            const int j = (int)(2 * group + hi);
+            unsigned sc, mn;
+            if (j < 4) {
+                sc = scl[j] & 63;
+                mn = scl[j + 4] & 63;
+            } else {
+                sc = (scl[j + 4] & 0x0F) | ((scl[j - 4] >> 6) << 4);
+                mn = (scl[j + 4] >> 4) | ((scl[j] >> 6) << 4);
+            }
+            const float d = orc_f16(blk), dmin = orc_f16(blk + 2);
+            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+            const uint8_t byte = blk[(type == 12 ? 16 : 48) + group * 32 + l];
+            float qv = (float)(hi ? (byte >> 4) : (byte & 0x0F));
+            if (type == 13) qv = qv + (((blk[16 + l] >> j) & 1) ? 16.0f : 0.0f);
+            const float p = d1 * qv;
+            v = p - m1;
         } else if (type == 14) {
             const uint8_t *blk = src + (i / 256) * 210;
             const int64_t k = i % 256, half = k / 128, r = k % 128, l = r % 32;

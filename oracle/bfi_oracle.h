@@ -32,10 +32,10 @@
  *                                  (cpu.rs:835-855) + numpy's sequential float32 accumulate
  *                                  and correctly rounded sqrt on random rows
  *   orc_dequant                    F16: all 65,536 codes against numpy's float16; BF16: against
- *                                  torch's bfloat16; Q8_0 / Q4_0 / Q6_K: the reference's KATs
- *                                  (q8_0.rs, q4_0.rs, q6_k.rs, types/mod.rs:300-328) and layouts
- *                                  with known small-integer values at every nibble, high-bit
- *                                  pair and scale position
+ *                                  torch's bfloat16; Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K: the
+ *                                  reference's KATs (q8_0.rs, q4_0.rs, q6_k.rs,
+ *                                  types/mod.rs:300-328) and encoder-built layouts with known
+ *                                  values at every nibble, high bit and (packed) scale
  *   orc_matmul_blocked             a closed form where block sums keep what one row sum loses
  *                                  (2^24 then 63 ones: 2^24 + 32 against 2^24)
  */

@@ -92,7 +92,7 @@ def test_qwen3_sized_head_and_fused_sampling(smp):
 
 # ---- quantized lm_head weights (bfi_smp_dequant, bfi_smp_head_typed) ---------------------------
 
-BLOCK = {1: (1, 2), 30: (1, 2), 8: (32, 34), 2: (32, 18), 14: (256, 210)}
+BLOCK = {1: (1, 2), 30: (1, 2), 8: (32, 34), 2: (32, 18), 14: (256, 210), 12: (256, 144), 13: (256, 176)}
 
 
 def _random_tensor(rng, ggml_type, n):
@@ -109,10 +109,12 @@ def _random_tensor(rng, ggml_type, n):
         raw[:, 0:2] = (rng.standard_normal(nb) * 0.01).astype(np.float16).view(np.uint8).reshape(nb, 2)
     elif ggml_type == 14:
         raw[:, 208:210] = (rng.standard_normal(nb) * 0.001).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif ggml_type in (12, 13):  # d and dmin
+        raw[:, 0:4] = (rng.standard_normal(2 * nb) * 0.001).astype(np.float16).view(np.uint8).reshape(nb, 4)
     return raw.reshape(-1)
 
 
-@pytest.mark.parametrize("ggml_type", [1, 30, 8, 2, 14])
+@pytest.mark.parametrize("ggml_type", [1, 30, 8, 2, 14, 12, 13])
 def test_device_dequant_matches_oracle(smp, ggml_type):
     import torch
 
@@ -128,7 +130,8 @@ def test_device_dequant_matches_oracle(smp, ggml_type):
     assert (np.isnan(g) == np.isnan(want)).all()
 
 
-@pytest.mark.parametrize("ggml_type,d", [(8, 256), (8, 1000), (2, 64), (14, 256), (1, 130), (30, 64)])
+@pytest.mark.parametrize("ggml_type,d", [(8, 256), (8, 1000), (2, 64), (14, 256), (12, 512), (13, 256), (1, 130),
+                                         (30, 64)])
 def test_typed_head_matches_oracle_bitwise(smp, ggml_type, d):
     """Q8_0 and Q4_0 rows of whole blocks take the block dot order, other rows one dot."""
     import torch
@@ -157,4 +160,4 @@ def test_dequant_rejects_partial_blocks_and_other_types(smp):
     with pytest.raises(bfi_smp.SamplerError):
         smp.dequant(8, src, 31)
     with pytest.raises(bfi_smp.SamplerError):
-        smp.dequant(12, src, 256)  # Q4_K: not taken
+        smp.dequant(41, src, 128)  # Q1_0: not taken

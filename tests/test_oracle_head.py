@@ -145,3 +145,44 @@ def test_blocked_dot_keeps_what_one_row_sum_loses():
     # a partial last block sums what it holds
     w2 = np.array([[1.0] * 40], np.float32)
     assert O.matmul_blocked(w2, np.ones((1, 40), np.float32), 32)[0, 0] == 40.0
+
+
+def _pack_scale_min_k4(sc, mn):
+    """12 bytes holding eight 6-bit scales and mins, the inverse of get_scale_min_k4
+    (k_scale.rs:3-11): sub-blocks 0-3 in the low 6 bits of bytes 0-7, sub-blocks 4-7 split
+    into low nibbles (bytes 8-11) and top two bits (the high bits of bytes 0-7)."""
+    q = np.zeros(12, np.uint8)
+    for j in range(4):
+        q[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        q[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        q[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    return q
+
+
+def test_dequant_k_quants_place_every_weight():
+    """Q4_K and Q5_K blocks from an encoder: d = 0.5, dmin = 0.25, scales and mins 1..63 spread
+    over all eight sub-blocks (so the packed high bits matter), nibble k % 16 at weight k and,
+    for Q5_K, the high bit set on every third weight; the reference's all-zero KAT."""
+    assert (O.dequant(12, np.zeros(144, np.uint8), 256) == 0.0).all()  # types/mod.rs:319-322
+    sc = np.array([1, 7, 33, 63, 18, 45, 60, 5])
+    mn = np.array([2, 62, 17, 9, 48, 31, 3, 40])
+    for t, bb in ((12, 144), (13, 176)):
+        blk = np.zeros(bb, np.uint8)
+        blk[0:2] = _f16_bytes(0.5)
+        blk[2:4] = _f16_bytes(0.25)
+        blk[4:16] = _pack_scale_min_k4(sc, mn)
+        qs = 16 if t == 12 else 48
+        want = []
+        for k in range(256):
+            group, r = divmod(k, 64)
+            hi, l = divmod(r, 32)
+            nib = k % 16
+            blk[qs + group * 32 + l] |= nib << (4 * hi)
+            extra = 0
+            if t == 13 and k % 3 == 0:
+                blk[16 + l] |= 1 << (2 * group + hi)
+                extra = 16
+            j = 2 * group + hi
+            want.append(np.float32(np.float32(0.5 * sc[j]) * np.float32(nib + extra)) - np.float32(0.25 * mn[j]))
+        got = O.dequant(t, blk, 256)
+        assert np.array_equal(got, np.array(want, np.float32)), t
