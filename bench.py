@@ -197,6 +197,17 @@ def bench_head(args):
                                                  dd["hist_off"]), steps, warm)
     flops = 2.0 * T * V * d
     achieved = flops / t_head / 1e12
+    # the same head over Q8_0 weights (a GGUF lm_head format): dequantized once, then the
+    # block dot order (each 32-weight block summed apart)
+    wq = (rng.standard_normal((V, d)) * (8 / np.sqrt(d))).astype(np.float32).reshape(-1, 32)
+    dq = np.maximum(np.abs(wq).max(1), 1e-8) / 127.0
+    q8 = np.zeros((wq.shape[0], 34), np.uint8)
+    q8[:, 0:2] = dq.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    q8[:, 2:] = np.clip(np.rint(wq / dq[:, None]), -127, 127).astype(np.int8).view(np.uint8)
+    src = torch.from_numpy(q8.reshape(-1)).to(dev)
+    w8 = torch.empty((V, d), dtype=torch.float32, device=dev)
+    t_deq = timed(lambda: smp.dequant(8, src, V * d, out=w8), 3, 1)
+    t_head_q8 = timed(lambda: smp.head_typed(x, nw, 1e-6, w8, 8, out=logits), steps, warm)
     xs = x[:1].cpu().numpy()
     ws = w.cpu().numpy()
     t0 = time.perf_counter()
@@ -205,6 +216,7 @@ def bench_head(args):
     line = {"metric": "device head + sample rows/sec (Qwen3-0.6B-shaped head, B=64)",
             "value": round(T / t_fused, 1), "unit": "rows/s", "n_gpus": 1, "higher_is_better": True,
             "head_ms": round(t_head * 1e3, 3), "head_sample_ms": round(t_fused * 1e3, 3),
+            "head_q8_0_ms": round(t_head_q8 * 1e3, 3), "dequant_q8_0_ms": round(t_deq * 1e3, 3),
             "readback_bytes_per_row": 4, "dtype": "f32", "data": "synthetic",
             "config": {"workload": "F2 head + sample", "rows": T, "n_embd": d, "n_vocab": V},
             "roofline": {"bound": "valu", "achieved": round(achieved, 2), "peak": 157.3, "unit": "TFLOP/s",
