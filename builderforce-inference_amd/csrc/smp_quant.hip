@@ -39,11 +39,18 @@ constexpr uint32_t UE_BIAS = 1024u;
 constexpr int QVMAX = 4;             // 16-byte vectors per thread
 constexpr int NSLOT = QVMAX * NWAVE;  // (vector, wave) slots of a chunk, in index order
 
-struct __align__(16) QuantSmem {
+// SHARED (the 16-byte, four-vector f32 chunks): the run table takes the history counts' space
+// (the counts are read before the first run is), so the workgroup fits 33 KB of LDS and four
+// workgroups share a CU; a first chunk's walk then reads its windows' terms from its items.
+template <bool SHARED>
+struct __align__(16) QuantSmemT {
     uint64_t etab[32];       // glibc's expf table (EXP2_32), per-lane reads from LDS
-    uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids (two 16-bit halves a word);
-                                 // in a row's first chunk, later: the windows' terms
-    uint32_t rq[QWIN + 1];   // per run: units
+    union {
+        uint32_t hc[CHUNK_MAX / 2];  // history counts of the chunk's ids (two 16-bit halves a word);
+                                     // in a row's first chunk, later: the windows' terms (not SHARED)
+        uint32_t rq_s[SHARED ? QWIN + 1 : 1];  // SHARED: per run, units
+    };
+    uint32_t rq_o[SHARED ? 1 : QWIN + 1];      // not SHARED: per run, units
     uint32_t rhi[QWIN + 1];  // per run: its unit exponent + 150 (0: no element)
     float vs[NSLOT];         // per (vector, wave): sum of the terms
     float vm[NSLOT];         // per (vector, wave): largest term (the running sum's lower bound)
@@ -51,9 +58,13 @@ struct __align__(16) QuantSmem {
     uint32_t wg[NWAVE];
     uint32_t wb[NWAVE];
     uint32_t gbase;
+    __device__ __forceinline__ uint32_t* rq() { return SHARED ? rq_s : rq_o; }
 };
 static_assert(NSLOT <= WAVE, "one lane per (vector, wave) slot");
 static_assert(QWIN <= CHUNK_MAX / 2, "a first chunk's window terms fit the history counts' space");
+
+template <class S> constexpr bool kSharedRq = false;
+template <> constexpr bool kSharedRq<QuantSmemT<true>> = true;
 
 __device__ __forceinline__ uint32_t lds_min(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_min((BFI_LDS uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -77,13 +88,15 @@ __device__ __forceinline__ void slot_prefix(const float* vs, const float* vm, in
     }
 }
 
-template <bool BF16, int QV, bool FULL>
-__device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int row, int chunk, uint32_t c0,
+template <bool BF16, int QV, bool FULL, class Smem>
+__device__ __forceinline__ void quant_chunk(const KArgs& a, Smem& sm, int row, int chunk, uint32_t c0,
                                             uint32_t c1);
 
 template <bool BF16, int QV>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void k_quant(KArgs a) {  // 3 workgroups per CU
-    __shared__ QuantSmem sm;
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(!BF16 && QV == 4 ? 8 : 6))) void k_quant(
+    KArgs a) {  // four workgroups per CU for the four-vector f32 chunks, else three
+    using Smem = QuantSmemT<!BF16 && QV == 4>;
+    __shared__ Smem sm;
     const uint32_t G = gridDim.x, bid = blockIdx.x;
     const uint32_t nc = (uint32_t)a.n_chunks;
     // each XCD takes a contiguous block [L0, L0 + size) of the (row, chunk) order (its rows'
@@ -113,9 +126,9 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(6))) void
     const uint32_t c0 = (uint32_t)chunk * (uint32_t)a.chunk;
     const uint32_t c1 = min(c0 + (uint32_t)a.chunk, V);
     if (a.vec_ok && c1 - c0 == (uint32_t)(BLOCK * QV * Elem<BF16>::EPV))
-        quant_chunk<BF16, QV, true>(a, sm, row, chunk, c0, c1);
+        quant_chunk<BF16, QV, true, Smem>(a, sm, row, chunk, c0, c1);
     else
-        quant_chunk<BF16, QV, false>(a, sm, row, chunk, c0, c1);
+        quant_chunk<BF16, QV, false, Smem>(a, sm, row, chunk, c0, c1);
 }
 
 // The terms e = expf(fl(x / T) - M) of a thread's elements, exactly as the reference
@@ -146,8 +159,8 @@ __device__ __forceinline__ void exact_terms(const float (&x)[QV][EPV], float (&e
         }
 }
 
-template <bool BF16, int QV, bool FULL>
-__device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int row, int chunk, uint32_t c0,
+template <bool BF16, int QV, bool FULL, class Smem>
+__device__ __forceinline__ void quant_chunk(const KArgs& a, Smem& sm, int row, int chunk, uint32_t c0,
                                             uint32_t c1) {
     constexpr int EPV = Elem<BF16>::EPV;
     static_assert(QV <= QVMAX, "per-vector tables");
@@ -456,12 +469,12 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
 #pragma unroll
                     for (int e = 1; e < EPV; e++) ee = e == i ? ev[q][e] : ee;
                     *reinterpret_cast<uint2*>(&items[pos]) = make_uint2(id0 + (uint32_t)i, __float_as_uint(ee));
-                    if (chunk == 0) sm.hc[pos] = __float_as_uint(ee);  // (for the walk below)
+                    if (!kSharedRq<Smem> && chunk == 0) sm.hc[pos] = __float_as_uint(ee);  // (for the walk below)
                     pos++;
                 }
             }
             for (uint32_t k = (uint32_t)tid; k <= nwin; k += BLOCK) {
-                sm.rq[k] = 0u;
+                sm.rq()[k] = 0u;
                 sm.rhi[k] = 0u;
             }
             __syncthreads();
@@ -493,7 +506,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                     }
                     const uint32_t k = wpre[q];
                     if (have && k != key) {
-                        lds_add(&sm.rq[key], acc);
+                        lds_add(&sm.rq()[key], acc);
                         lds_max(&sm.rhi[key], khi);
                         bad |= (acc != 0u && klo != khi) ? 1u : 0u;
                         nflush++;
@@ -513,7 +526,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                     if (((wmq | zmq) >> e) & 1u) continue;
                     const uint32_t k = wpre[q] + (uint32_t)__popc(wmq & ((1u << e) - 1u));
                     if (have && k != key) {
-                        lds_add(&sm.rq[key], acc);
+                        lds_add(&sm.rq()[key], acc);
                         lds_max(&sm.rhi[key], khi);
                         bad |= (acc != 0u && klo != khi) ? 1u : 0u;
                         nflush++;
@@ -544,12 +557,12 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                         wave_scan_incl(have ? khi : 0u, 0u, [](uint32_t u, uint32_t v) { return max(u, v); }));
                     bad |= (s != 0u && l != h) ? 1u : 0u;
                     if (lane == 0) {
-                        lds_add(&sm.rq[k0], s);
+                        lds_add(&sm.rq()[k0], s);
                         lds_max(&sm.rhi[k0], h);
                     }
                 }
             } else if (have) {
-                lds_add(&sm.rq[key], acc);
+                lds_add(&sm.rq()[key], acc);
                 lds_max(&sm.rhi[key], khi);
             }
             __threadfence_block();
@@ -557,7 +570,7 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
             // the items' runs (the window halves are written): the run before each window
             // element, then the tail run
             for (uint32_t k = (uint32_t)tid; k <= nwin; k += BLOCK) {
-                const uint32_t q = sm.rq[k];
+                const uint32_t q = sm.rq()[k];
                 const uint32_t hi = sm.rhi[k];
                 const int32_t ue = hi ? (int32_t)hi - 150 : -(int32_t)UE_BIAS;  // empty: any binade
                 if (k < nwin) *reinterpret_cast<uint2*>(&items[k].q) = make_uint2(q, (uint32_t)ue);
@@ -618,7 +631,8 @@ __device__ __forceinline__ void quant_chunk(const KArgs& a, QuantSmem& sm, int r
                 [&](uint32_t j) {
                     const uint32_t hi = sm.rhi[j];
                     const bool el = j < qn;
-                    return QItem{el ? 0u : QI_NONE, el ? __uint_as_float(sm.hc[j]) : 0.0f, sm.rq[j],
+                    const float ej = kSharedRq<Smem> ? *(const BFI_GLB float*)&items[j].e : __uint_as_float(sm.hc[j]);
+                return QItem{el ? 0u : QI_NONE, el ? ej : 0.0f, sm.rq()[j],
                                  hi ? (int32_t)hi - 150 : -(int32_t)UE_BIAS};
                 },
                 0u, n, (uint32_t)a.V, m, ue);
