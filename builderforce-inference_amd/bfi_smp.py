@@ -68,6 +68,8 @@ def lib():
         L.bfi_smp_head.argtypes = [P, P, P, I32, ctypes.c_float, P, I64, I64, I64, P, P]
         L.bfi_smp_dequant.argtypes = [P, I32, P, I64, P, P]
         L.bfi_smp_head_typed.argtypes = [P, P, P, I32, ctypes.c_float, P, I32, I64, I64, I64, P, P]
+        L.bfi_smp_head_typed_sample_rows.argtypes = [P, P, P, I32, ctypes.c_float, P, I32, I64, I64, I64, P, P, P,
+                                                     P, I64, P, P, P]
         L.bfi_smp_head_sample_rows.argtypes = [P, P, P, I32, ctypes.c_float, P, I64, I64, I64, P, P, P, P, I64, P, P,
                                                P]
         L.bfi_rng_next_u64.argtypes = [P]
@@ -328,6 +330,19 @@ class Sampler:
                                         ctypes.c_float(eps), _dptr(w), int(ggml_type), T, d, V, _dptr(out),
                                         self._stream(stream))
         self._check(rc, "bfi_smp_head_typed")
+        return out
+
+    def head_typed_sample_rows(self, x, norm_w, eps, w, ggml_type, params, u, out, hist=None, hist_off=None,
+                               mask=None, norm_per_row=False, stream=None):
+        """The fused device step over weights dequantized from GGML type ggml_type."""
+        T, d = x.shape
+        V = w.shape[0]
+        ms = 0 if mask is None else mask.stride(0)
+        rc = self._L.bfi_smp_head_typed_sample_rows(self._ctx, _dptr(x), _dptr(norm_w), 1 if norm_per_row else 0,
+                                                    ctypes.c_float(eps), _dptr(w), int(ggml_type), T, d, V,
+                                                    _dptr(params), _dptr(hist), _dptr(hist_off), _dptr(mask), ms,
+                                                    _dptr(u), _dptr(out), self._stream(stream))
+        self._check(rc, "bfi_smp_head_typed_sample_rows")
         return out
 
     def head_sample_rows(self, x, norm_w, eps, w, params, u, out, hist=None, hist_off=None, mask=None,

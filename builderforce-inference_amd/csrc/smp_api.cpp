@@ -680,10 +680,22 @@ int bfi_smp_head_sample_rows(bfi_smp_ctx* ctx, const float* d_x, const float* d_
                              const bfi_smp_row_params* d_params, const uint32_t* d_hist, const int64_t* d_hist_off,
                              const uint32_t* d_mask, int64_t mask_stride, const float* d_u, uint32_t* d_out,
                              void* stream) {
+    return bfi_smp_head_typed_sample_rows(ctx, d_x, d_norm_w, norm_per_row, eps, d_w, 0, n_tokens, n_embd, n_vocab,
+                                          d_params, d_hist, d_hist_off, d_mask, mask_stride, d_u, d_out, stream);
+}
+
+int bfi_smp_head_typed_sample_rows(bfi_smp_ctx* ctx, const float* d_x, const float* d_norm_w, int norm_per_row,
+                                   float eps, const float* d_w, int32_t ggml_type, int64_t n_tokens, int64_t n_embd,
+                                   int64_t n_vocab, const bfi_smp_row_params* d_params, const uint32_t* d_hist,
+                                   const int64_t* d_hist_off, const uint32_t* d_mask, int64_t mask_stride,
+                                   const float* d_u, uint32_t* d_out, void* stream) {
     if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
+    if (ggml_block_elems(ggml_type) == 0)
+        return fail(ctx, BFI_SMP_EINVAL, "GGML type %d is not one this head takes", (int)ggml_type);
+    const int blocked = (ggml_type == 8 || ggml_type == 2) && n_embd % 32 == 0;
     const size_t lbytes = (size_t)(n_tokens > 0 ? n_tokens : 0) * (size_t)(n_vocab > 0 ? n_vocab : 0) * sizeof(float);
     int rc = run_head(ctx, d_x, d_norm_w, norm_per_row, eps, d_w, n_tokens, n_embd, n_vocab, nullptr, lbytes,
-                      (hipStream_t)stream);
+                      (hipStream_t)stream, blocked);
     if (rc != BFI_SMP_OK) return rc;
     return bfi_smp_sample_rows(ctx, ctx->head, BFI_SMP_F32, n_tokens, n_vocab, n_vocab, d_params, d_hist, d_hist_off,
                                d_mask, mask_stride, d_u, d_out, stream);

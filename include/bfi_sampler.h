@@ -249,6 +249,16 @@ int bfi_smp_head_typed(bfi_smp_ctx *ctx, const float *d_x, const float *d_norm_w
                        float eps, const float *d_w, int32_t ggml_type, int64_t n_tokens,
                        int64_t n_embd, int64_t n_vocab, float *d_logits, void *stream);
 
+/* bfi_smp_head_sample_rows over weights dequantized from ggml_type (bfi_smp_head_typed's
+ * order): the fused decode step of a GGUF model with a quantized lm_head. */
+int bfi_smp_head_typed_sample_rows(bfi_smp_ctx *ctx, const float *d_x, const float *d_norm_w,
+                                   int norm_per_row, float eps, const float *d_w, int32_t ggml_type,
+                                   int64_t n_tokens, int64_t n_embd, int64_t n_vocab,
+                                   const bfi_smp_row_params *d_params, const uint32_t *d_hist,
+                                   const int64_t *d_hist_off, const uint32_t *d_mask,
+                                   int64_t mask_stride, const float *d_u, uint32_t *d_out,
+                                   void *stream);
+
 /* ---- host-side helpers (no GPU work) ------------------------------------ */
 
 /* xorshift64 step of `Rng::next_u64` (sample.rs:445-455); updates *state. */

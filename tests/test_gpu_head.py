@@ -161,3 +161,32 @@ def test_dequant_rejects_partial_blocks_and_other_types(smp):
         smp.dequant(8, src, 31)
     with pytest.raises(bfi_smp.SamplerError):
         smp.dequant(41, src, 128)  # Q1_0: not taken
+
+
+def test_typed_fused_step_draws_the_oracles_tokens(smp):
+    """A Q8_0 lm_head (n_embd 256, 20,000 ids): head_typed_sample_rows draws the tokens the oracle
+    samples from the oracle's block-order logits."""
+    import torch
+
+    rng = np.random.default_rng(21)
+    T, d, V = 4, 256, 20000
+    x = (rng.standard_normal((T, d)) * 3).astype(np.float32)
+    nw = rng.standard_normal(d).astype(np.float32)
+    src = _random_tensor(rng, 8, V * d)
+    src.reshape(-1, 34)[:, 0:2] = (np.abs(rng.standard_normal(V * d // 32)) * 0.05 + 0.01).astype(
+        np.float16).view(np.uint8).reshape(-1, 2)  # (peaked rows)
+    wd = smp.dequant(8, _dev(src), V * d).view(V, d)
+    w = O.dequant(8, src, V * d).reshape(V, d)
+    logits = O.matmul_blocked(w, O.rms_norm(x, nw, 1e-6), 32)
+    rows = [dict(temperature=0.8, top_p=0.95), dict(temperature=0.0), dict(temperature=1.0, top_k=40, min_p=0.05),
+            dict(temperature=0.6, top_p=0.9, repeat_penalty=1.1)]
+    params = bfi_smp.params_array(rows)
+    hist = rng.integers(0, V, 32).astype(np.uint32)
+    off = np.array([0, 8, 16, 24, 32], np.int64)
+    u = rng.random(T).astype(np.float32)
+    out = torch.zeros(T, dtype=torch.int32, device="cuda:0")
+    pd = torch.from_numpy(params.view(np.uint8)).to("cuda:0")
+    smp.head_typed_sample_rows(_dev(x), _dev(nw), 1e-6, wd, 8, pd, _dev(u), out, _dev(hist.view(np.int32)), _dev(off))
+    torch.cuda.synchronize()
+    want = O.sample_rows(logits, params, hist, off, u)
+    assert out.cpu().numpy().astype(np.uint32).tolist() == [int(t) for t in want]
