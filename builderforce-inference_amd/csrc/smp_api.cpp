@@ -631,8 +631,19 @@ int64_t ggml_block_elems(int32_t type) {
         case 0: case 1: case 30: return 1;  // F32, F16, BF16
         case 2: case 8: return 32;           // Q4_0, Q8_0
         case 12: case 13: case 14: return 256;  // Q4_K, Q5_K, Q6_K
+        case 41: case 142: case 143: return 128;  // Q1_0, PQ2_0, PTQ1_0
         default: return 0;
     }
+}
+
+// The head's dot order for a type (cpu.rs:515-563): a format with a fused block dot sums by
+// blocks when the row is whole blocks (1: 32-weight blocks, 2: 128-weight blocks, 3: Q1_0's
+// signed blocks); every other type, and a row of partial blocks, is one dot over the row (0).
+int head_mode(int32_t type, int64_t n_embd) {
+    if ((type == 8 || type == 2) && n_embd % 32 == 0) return 1;
+    if ((type == 142 || type == 143) && n_embd % 128 == 0) return 2;
+    if (type == 41 && n_embd % 128 == 0) return 3;
+    return 0;
 }
 
 }  // namespace
@@ -660,9 +671,7 @@ int bfi_smp_head_typed(bfi_smp_ctx* ctx, const float* d_x, const float* d_norm_w
     if (!d_logits) return fail(ctx, BFI_SMP_EINVAL, "d_logits is NULL");
     if (ggml_block_elems(ggml_type) == 0)
         return fail(ctx, BFI_SMP_EINVAL, "GGML type %d is not one this head takes", (int)ggml_type);
-    // cpu.rs:515-563: the types with a fused block dot (Q8_0, Q4_0) sum by blocks when the row
-    // is whole blocks; every other type, and a row of partial blocks, is one dot over the row
-    const int blocked = (ggml_type == 8 || ggml_type == 2) && n_embd % 32 == 0;
+    const int blocked = head_mode(ggml_type, n_embd);
     return run_head(ctx, d_x, d_norm_w, norm_per_row, eps, d_w, n_tokens, n_embd, n_vocab, d_logits, 0,
                     (hipStream_t)stream, blocked);
 }
@@ -692,7 +701,7 @@ int bfi_smp_head_typed_sample_rows(bfi_smp_ctx* ctx, const float* d_x, const flo
     if (!ctx) return fail(nullptr, BFI_SMP_EINVAL, "ctx is NULL");
     if (ggml_block_elems(ggml_type) == 0)
         return fail(ctx, BFI_SMP_EINVAL, "GGML type %d is not one this head takes", (int)ggml_type);
-    const int blocked = (ggml_type == 8 || ggml_type == 2) && n_embd % 32 == 0;
+    const int blocked = head_mode(ggml_type, n_embd);
     const size_t lbytes = (size_t)(n_tokens > 0 ? n_tokens : 0) * (size_t)(n_vocab > 0 ? n_vocab : 0) * sizeof(float);
     int rc = run_head(ctx, d_x, d_norm_w, norm_per_row, eps, d_w, n_tokens, n_embd, n_vocab, nullptr, lbytes,
                       (hipStream_t)stream, blocked);

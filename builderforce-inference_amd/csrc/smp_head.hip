@@ -60,7 +60,8 @@ __global__ __launch_bounds__(HN_BLOCK) void k_head_norm(const float* __restrict_
 // F16 and BF16 widen exactly; Q8_0 is q * d, Q4_0 (nibble - 8) * d, Q6_K (d * scale) * q, Q4_K
 // and Q5_K (d * scale) * q - dmin * min, each product and difference one f32 rounding, d an
 // f16 widened exactly. One thread per weight.
-constexpr int GT_F16 = 1, GT_Q4_0 = 2, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q5_K = 13, GT_Q6_K = 14, GT_BF16 = 30;
+constexpr int GT_F16 = 1, GT_Q4_0 = 2, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q5_K = 13, GT_Q6_K = 14, GT_BF16 = 30, GT_Q1_0 = 41,
+              GT_PQ2_0 = 142, GT_PTQ1_0 = 143;
 
 // The 6-bit scale and min of sub-block j of a K-quant block (k_scale.rs:3-11).
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint32_t& sc, uint32_t& m) {
@@ -110,6 +111,26 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src
         float qv = (float)(hi ? (byte >> 4) : (byte & 0x0F));
         if (TYPE == GT_Q5_K) qv = qv + (((b[16 + l] >> (2 * group + hi)) & 1u) ? 16.0f : 0.0f);
         v = (f16_at(b) * (float)sc) * qv - f16_at(b + 2) * (float)m;
+    } else if (TYPE == GT_Q1_0) {  // q1_0.rs:34-45: 18-byte blocks of 128, sign bits LSB first
+        const uint8_t* b = src + (i / 128) * 18;
+        const int k = (int)(i % 128);
+        const float d = f16_at(b);
+        v = ((b[2 + k / 8] >> (k % 8)) & 1) ? d : -d;
+    } else if (TYPE == GT_PQ2_0) {  // pq2_0.rs:26-36: 34-byte blocks of 128, 2-bit codes LSB first
+        const uint8_t* b = src + (i / 128) * 34;
+        const int k = (int)(i % 128);
+        v = ((float)((b[2 + k / 4] >> (2 * (k % 4))) & 3) - 1.0f) * f16_at(b);
+    } else if (TYPE == GT_PTQ1_0) {
+        // ptq1_0.rs:30-75: 28-byte blocks (qs[24], qh[2], d); weight k is base-3 digit n of a
+        // byte, read as ((u8)(byte * 3^n) * 3) >> 8: k < 80 digit k/16 of qs[k%16], k < 120
+        // digit (k-80)/8 of qs[16 + (k-80)%8], else digit (k-120)/2 of qh[(k-120)%2]
+        const uint8_t* b = src + (i / 128) * 28;
+        const int k = (int)(i % 128);
+        const int at = k < 80 ? k % 16 : k < 120 ? 16 + (k - 80) % 8 : 24 + (k - 120) % 2;
+        const int n = k < 80 ? k / 16 : k < 120 ? (k - 80) / 8 : (k - 120) / 2;
+        const uint32_t p3 = n == 0 ? 1u : n == 1 ? 3u : n == 2 ? 9u : n == 3 ? 27u : 81u;
+        const uint32_t trit = (((uint32_t)b[at] * p3) & 0xFFu) * 3u >> 8;
+        v = ((float)trit - 1.0f) * f16_at(b + 26);
     } else {  // GT_Q6_K, q6_k.rs:4-29: 210-byte blocks of 256 (ql[128], qh[64], scales[16], d)
         const uint8_t* b = src + (i / 256) * 210;
         const int k = (int)(i % 256), nh = k / 128, quarter = (k % 128) / 32, l = k % 32;
@@ -130,10 +151,13 @@ constexpr int HG_BLOCK = 256;
 
 // out[t][o] = sum over i in index order of W[o][i] * X[t][i]. A thread owns 4 outputs x 4
 // tokens; each chunk of 16 inner positions is staged transposed in LDS so a thread reads
-// its 4 weights and 4 inputs of one position as two 16-byte loads. BLOCKED: the fused block
-// dot of the Q8_0 and Q4_0 formats (q8_0.rs:11-15, cpu.rs:550-563): each 32-weight block's
-// products summed from -0.0, the block sums added from +0.0 (d a multiple of 32).
-template <bool BLOCKED>
+// its 4 weights and 4 inputs of one position as two 16-byte loads. BLK > 0: the fused block
+// dot of the Q8_0 and Q4_0 (BLK 32), PQ2_0 and PTQ1_0 (BLK 128) formats (q8_0.rs:11-15,
+// pq2_0.rs:38-42, cpu.rs:550-563): each block's products summed from -0.0, the block sums
+// added from +0.0 (d a multiple of BLK). SIGNS: the Q1_0 dot (q1_0.rs:48-64, simd.rs:74-80)
+// over its dequantized weights +-s: each input added with its weight's sign, the block's sum
+// times the block's scale |w| (BLK 128).
+template <int BLK, bool SIGNS>
 __global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict__ W, const float* __restrict__ X,
                                                         int64_t n_out, int64_t n_tok, int64_t d, int vec,
                                                         float* __restrict__ out) {
@@ -142,7 +166,10 @@ __global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict_
     const int tid = threadIdx.x;
     const int to = tid % 16, tt = tid / 16;  // this thread: outputs 4 to.., tokens 4 tt..
     const int64_t o0 = (int64_t)blockIdx.x * HG_BO, t0 = (int64_t)blockIdx.y * HG_BT;
+    constexpr bool BLOCKED = BLK > 0;
+    static_assert(BLK % HG_K == 0 && (!SIGNS || BLOCKED), "a block is whole chunks");
     float acc[4][4], part[4][4];  // (part: the current block's sum, BLOCKED)
+    float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // (SIGNS: the block's scale of each output)
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
@@ -179,20 +206,27 @@ __global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict_
         for (int k = 0; k < kn; k++) {
             const float4 a = Ws[k][to], b = Xs[k][tt];
             const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+            if (SIGNS && k == 0 && k0 % BLK == 0) {
+#pragma unroll
+                for (int p = 0; p < 4; p++) bs[p] = __builtin_fabsf(av[p]);
+            }
 #pragma unroll
             for (int p = 0; p < 4; p++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    if (BLOCKED) part[p][q] = part[p][q] + av[p] * bv[q];
+                    if (SIGNS)  // (x with the weight's sign bit: exact negation where it is set)
+                        part[p][q] = part[p][q] + __uint_as_float(__float_as_uint(bv[q]) ^
+                                                                  (__float_as_uint(av[p]) & 0x80000000u));
+                    else if (BLOCKED) part[p][q] = part[p][q] + av[p] * bv[q];
                     else acc[p][q] = acc[p][q] + av[p] * bv[q];
                 }
         }
-        if (BLOCKED && ((k0 + HG_K) % 32) == 0) {  // (a block ends with every other chunk)
+        if (BLOCKED && ((k0 + HG_K) % BLK) == 0) {  // (the chunk ends a block)
 #pragma unroll
             for (int p = 0; p < 4; p++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    acc[p][q] = acc[p][q] + part[p][q];
+                    acc[p][q] = acc[p][q] + (SIGNS ? part[p][q] * bs[p] : part[p][q]);
                     part[p][q] = -0.0f;
                 }
         }
@@ -213,15 +247,22 @@ __global__ __launch_bounds__(HG_BLOCK) void k_head_gemm(const float* __restrict_
 
 // xn: n_tok * d floats of workspace; out: n_tok * n_out logits.
 // vec: d % 4 == 0 and W 16-byte aligned (the rows then load as 16-byte vectors).
-// blocked: the Q8_0 / Q4_0 block dot order (d % 32 == 0).
+// blocked: the dot order of a format with a fused block dot: 1 blocks of 32 (Q8_0, Q4_0;
+// d % 32 == 0), 2 blocks of 128 (PQ2_0, PTQ1_0), 3 Q1_0's signed blocks of 128 (d % 128 == 0).
 hipError_t launch_head(const float* x, const float* norm_w, int norm_per_row, float eps, const float* W,
                        int64_t n_tok, int64_t d, int64_t n_out, int vec, int blocked, float* xn, float* out,
                        hipStream_t stream) {
     if (n_tok <= 0 || n_out <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_head_norm, dim3((unsigned)n_tok), dim3(HN_BLOCK), 0, stream, x, norm_w, norm_per_row, eps, d, xn);
     const dim3 grid((unsigned)((n_out + HG_BO - 1) / HG_BO), (unsigned)((n_tok + HG_BT - 1) / HG_BT));
-    if (blocked) hipLaunchKernelGGL(k_head_gemm<true>, grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out);
-    else hipLaunchKernelGGL(k_head_gemm<false>, grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out);
+    if ((blocked == 1 && d % 32 != 0) || (blocked >= 2 && d % 128 != 0) || blocked < 0 || blocked > 3)
+        return hipErrorInvalidValue;
+    switch (blocked) {
+        case 1: hipLaunchKernelGGL((k_head_gemm<32, false>), grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out); break;
+        case 2: hipLaunchKernelGGL((k_head_gemm<128, false>), grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out); break;
+        case 3: hipLaunchKernelGGL((k_head_gemm<128, true>), grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out); break;
+        default: hipLaunchKernelGGL((k_head_gemm<0, false>), grid, dim3(HG_BLOCK), 0, stream, W, xn, n_out, n_tok, d, vec, out);
+    }
     return hipGetLastError();
 }
 
@@ -239,6 +280,9 @@ hipError_t launch_dequant(int type, const void* src, int64_t n, float* dst, hipS
         case GT_Q6_K: hipLaunchKernelGGL(k_dequant<GT_Q6_K>, grid, dim3(256), 0, stream, s, n, dst); break;
         case GT_Q4_K: hipLaunchKernelGGL(k_dequant<GT_Q4_K>, grid, dim3(256), 0, stream, s, n, dst); break;
         case GT_Q5_K: hipLaunchKernelGGL(k_dequant<GT_Q5_K>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_Q1_0: hipLaunchKernelGGL(k_dequant<GT_Q1_0>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_PQ2_0: hipLaunchKernelGGL(k_dequant<GT_PQ2_0>, grid, dim3(256), 0, stream, s, n, dst); break;
+        case GT_PTQ1_0: hipLaunchKernelGGL(k_dequant<GT_PTQ1_0>, grid, dim3(256), 0, stream, s, n, dst); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -230,7 +230,8 @@ int bfi_smp_head_sample_rows(bfi_smp_ctx *ctx, const float *d_x, const float *d_
  * it (crates/bfi-gguf/src/types/, one file a format; replaces `dequant_tensor`, types/mod.rs, as
  * `matmul_quant` uses it, crates/bfi-core/src/cpu.rs:515-563): ggml_type 1 (F16), 30 (BF16),
  * 8 (Q8_0: q * d), 2 (Q4_0: (nibble - 8) * d), 14 (Q6_K: (d * scale) * q), 12 and 13 (Q4_K,
- * Q5_K: (d * scale) * q - dmin * min). A model's lm_head is dequantized once, at load.
+ * Q5_K: (d * scale) * q - dmin * min), 41 (Q1_0: +-d), 142 (PQ2_0: (code - 1) * d), 143 (PTQ1_0:
+ * (trit - 1) * d). A model's lm_head is dequantized once, at load.
  * BFI_SMP_EINVAL for another type or a partial block.
  */
 int bfi_smp_dequant(bfi_smp_ctx *ctx, int32_t ggml_type, const void *d_src, int64_t n_weights,
@@ -241,8 +242,11 @@ int bfi_smp_dequant(bfi_smp_ctx *ctx, int32_t ggml_type, const void *d_src, int6
  * output; 0 for f32 weights), in the dot order `matmul_quant` uses for that type
  * (cpu.rs:515-563): Q8_0 and Q4_0 have a fused block dot (q8_0.rs:11-15, q4_0.rs:14-18) — each
  * 32-weight block's products summed from -0.0, the block sums added from +0.0 — when n_embd is
- * a multiple of 32; F16, BF16, Q4_K, Q5_K, Q6_K (no block dot) and rows of partial blocks take
- * one dot over the row, as f32 weights do. Logits bit-identical to the reference's for that
+ * a multiple of 32; PQ2_0 and PTQ1_0 the same over 128-weight blocks (pq2_0.rs:38-42,
+ * ptq1_0.rs:72-76); Q1_0 (q1_0.rs:48-64, simd.rs:74-80) adds each block's inputs with their
+ * weight's sign from +0.0 and multiplies that sum by the block's scale (n_embd a multiple of
+ * 128); F16, BF16, Q4_K, Q5_K, Q6_K (no block dot) and rows of partial blocks take one dot over
+ * the row, as f32 weights do. Logits bit-identical to the reference's for that
  * tensor.
  */
 int bfi_smp_head_typed(bfi_smp_ctx *ctx, const float *d_x, const float *d_norm_w, int norm_per_row,

@@ -723,7 +723,7 @@ static float orc_f16(const uint8_t *p) {
 }
 
 /* dequant_row of each type, for n weights (whole blocks): f16.rs, bf16.rs, q8_0.rs:4-9,
- * q4_0.rs:4-12, q4_k.rs:6-29, q5_k.rs:6-36, q6_k.rs:4-29. Returns 0, or -1 for a type not
+ * q4_0.rs:4-12, q4_k.rs:6-29, q5_k.rs:6-36, q6_k.rs:4-29, q1_0.rs, pq2_0.rs, ptq1_0.rs. Returns 0, or -1 for a type not
  * restated. */
 int orc_dequant(int type, const uint8_t *src, int64_t n, float *dst) {
     for (int64_t i = 0; i < n; i++) {
@@ -785,6 +785,38 @@ int orc_dequant(int type, const uint8_t *src, int64_t n, float *dst) {
                 s = (float)(int8_t)sc[l / 16 + 6];
             }
             v = d * s * (float)q;
+        } else if (type == 41) {
+            /* q1_0.rs:34-45: 18-byte blocks of 128, sign bits LSB first, set +d, clear -d */
+            const uint8_t *blk = src + (i / 128) * 18;
+            const int64_t j = i % 128;
+            const float d = orc_f16(blk);
+            v = ((blk[2 + j / 8] >> (j % 8)) & 1) ? d : -d;
+        } else if (type == 142) {
+            /* pq2_0.rs:26-36: 34-byte blocks of 128, 2-bit codes LSB first, (code - 1) * d */
+            const uint8_t *blk = src + (i / 128) * 34;
+            const int64_t j = i % 128;
+            v = ((float)((blk[2 + j / 4] >> (2 * (j % 4))) & 3) - 1.0f) * orc_f16(blk);
+        } else if (type == 143) {
+            /* ptq1_0.rs:30-75: 28-byte blocks (qs[24], qh[2], d), base-3 digits read by
+             * multiplying; weights 0..79 are digit j/16 of qs[j%16], 80..119 digit (j-80)/8 of
+             * qs[16 + (j-80)%8], 120..127 digit (j-120)/2 of qh[(j-120)%2] */
+            static const unsigned pow3[5] = {1, 3, 9, 27, 81};
+            const uint8_t *blk = src + (i / 128) * 28;
+            const int64_t j = i % 128;
+            uint8_t byte;
+            unsigned dig;
+            if (j < 80) {
+                byte = blk[j % 16];
+                dig = (unsigned)(j / 16);
+            } else if (j < 120) {
+                byte = blk[16 + (j - 80) % 8];
+                dig = (unsigned)((j - 80) / 8);
+            } else {
+                byte = blk[24 + (j - 120) % 2];
+                dig = (unsigned)((j - 120) / 2);
+            }
+            const unsigned trit = ((unsigned)(uint8_t)(byte * pow3[dig]) * 3u) >> 8;
+            v = ((float)trit - 1.0f) * orc_f16(blk + 26);
         } else {
             return -1;
         }
@@ -811,6 +843,24 @@ void orc_matmul_blocked(const float *w, const float *x, int64_t n_tokens, int64_
                 float p = -0.0f;
                 for (int64_t i = b; i < b + block && i < n_in; i++) p = p + wr[i] * xr[i];
                 s = s + p;
+            }
+            out[t * n_out + o] = s;
+        }
+}
+
+/* The Q1_0 row dot (cpu.rs:550-553, simd.rs:74-80, q1_0.rs:48-64) over dequantized weights
+ * (+-d): per block of `block` the activations added from +0.0 with the sign of their weight,
+ * that sum times the block's scale |w|, the blocks added from +0.0. */
+void orc_matmul_signs(const float *w, const float *x, int64_t n_tokens, int64_t n_out, int64_t n_in,
+                      int64_t block, float *out) {
+    for (int64_t t = 0; t < n_tokens; t++)
+        for (int64_t o = 0; o < n_out; o++) {
+            const float *wr = w + o * n_in, *xr = x + t * n_in;
+            float s = 0.0f;
+            for (int64_t b = 0; b < n_in; b += block) {
+                float p = 0.0f;
+                for (int64_t i = b; i < b + block && i < n_in; i++) p = signbit(wr[i]) ? p - xr[i] : p + xr[i];
+                s = s + p * fabsf(wr[b]);
             }
             out[t * n_out + o] = s;
         }

@@ -35,9 +35,15 @@
  *                                  torch's bfloat16; Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K: the
  *                                  reference's KATs (q8_0.rs, q4_0.rs, q6_k.rs,
  *                                  types/mod.rs:300-328) and encoder-built layouts with known
- *                                  values at every nibble, high bit and (packed) scale
+ *                                  values at every nibble, high bit and (packed) scale;
+ *                                  Q1_0 / PQ2_0 / PTQ1_0: the reference's KATs (q1_0.rs,
+ *                                  pq2_0.rs, ptq1_0.rs tests) and a base-3 encoder's blocks
+ *                                  decoded back at every weight
  *   orc_matmul_blocked             a closed form where block sums keep what one row sum loses
  *                                  (2^24 then 63 ones: 2^24 + 32 against 2^24)
+ *   orc_matmul_signs               the same closed form through the scale (a block of ones
+ *                                  summed before its scale of 2^-7) and a product-first sum
+ *                                  that differs from it
  */
 #ifndef BFI_ORACLE_H
 #define BFI_ORACLE_H
@@ -119,6 +125,8 @@ void orc_matmul_f32(const float *w, const float *x, int64_t n_tokens, int64_t n_
 int orc_dequant(int type, const uint8_t *src, int64_t n, float *dst);
 void orc_matmul_blocked(const float *w, const float *x, int64_t n_tokens, int64_t n_out, int64_t n_in,
                         int64_t block, float *out);
+void orc_matmul_signs(const float *w, const float *x, int64_t n_tokens, int64_t n_out, int64_t n_in,
+                      int64_t block, float *out);
 
 #ifdef __cplusplus
 }

@@ -131,6 +131,8 @@ def lib(path=None):
         L.orc_dequant.restype = ctypes.c_int
         L.orc_matmul_blocked.argtypes = [P, P, I64, I64, I64, I64, P]
         L.orc_matmul_blocked.restype = None
+        L.orc_matmul_signs.argtypes = [P, P, I64, I64, I64, I64, P]
+        L.orc_matmul_signs.restype = None
         L.orc_verify_seq.argtypes = [
             P, ctypes.c_int, I64, I64, P, P, ctypes.c_size_t, P, ctypes.c_size_t, P, I64, P,
             ctypes.c_float, P, P,
@@ -174,6 +176,16 @@ def matmul_blocked(w, x, block: int):
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty((x.shape[0], w.shape[0]), np.float32)
     lib().orc_matmul_blocked(_ptr(w), _ptr(x), x.shape[0], w.shape[0], w.shape[1], int(block), _ptr(out))
+    return out
+
+
+def matmul_signs(w, x, block: int = 128):
+    """The Q1_0 row dot (simd.rs:74-80, q1_0.rs:48-64) over dequantized weights (+-d): each
+    block's activations summed with their weight's sign, times the block's scale."""
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty((x.shape[0], w.shape[0]), np.float32)
+    lib().orc_matmul_signs(_ptr(w), _ptr(x), x.shape[0], w.shape[0], w.shape[1], int(block), _ptr(out))
     return out
 
 

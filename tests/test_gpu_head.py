@@ -92,7 +92,8 @@ def test_qwen3_sized_head_and_fused_sampling(smp):
 
 # ---- quantized lm_head weights (bfi_smp_dequant, bfi_smp_head_typed) ---------------------------
 
-BLOCK = {1: (1, 2), 30: (1, 2), 8: (32, 34), 2: (32, 18), 14: (256, 210), 12: (256, 144), 13: (256, 176)}
+BLOCK = {1: (1, 2), 30: (1, 2), 8: (32, 34), 2: (32, 18), 14: (256, 210), 12: (256, 144), 13: (256, 176), 41: (128, 18),
+         142: (128, 34), 143: (128, 28)}
 
 
 def _random_tensor(rng, ggml_type, n):
@@ -107,6 +108,10 @@ def _random_tensor(rng, ggml_type, n):
         raw = top.view(np.uint8).reshape(nb, bb)
     elif ggml_type in (8, 2):
         raw[:, 0:2] = (rng.standard_normal(nb) * 0.01).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif ggml_type in (41, 142):
+        raw[:, 0:2] = (rng.standard_normal(nb) * 0.01).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif ggml_type == 143:
+        raw[:, 26:28] = (rng.standard_normal(nb) * 0.01).astype(np.float16).view(np.uint8).reshape(nb, 2)
     elif ggml_type == 14:
         raw[:, 208:210] = (rng.standard_normal(nb) * 0.001).astype(np.float16).view(np.uint8).reshape(nb, 2)
     elif ggml_type in (12, 13):  # d and dmin
@@ -114,7 +119,7 @@ def _random_tensor(rng, ggml_type, n):
     return raw.reshape(-1)
 
 
-@pytest.mark.parametrize("ggml_type", [1, 30, 8, 2, 14, 12, 13])
+@pytest.mark.parametrize("ggml_type", [1, 30, 8, 2, 14, 12, 13, 41, 142, 143])
 def test_device_dequant_matches_oracle(smp, ggml_type):
     import torch
 
@@ -131,9 +136,10 @@ def test_device_dequant_matches_oracle(smp, ggml_type):
 
 
 @pytest.mark.parametrize("ggml_type,d", [(8, 256), (8, 1000), (2, 64), (14, 256), (12, 512), (13, 256), (1, 130),
-                                         (30, 64)])
+                                         (30, 64), (41, 256), (41, 224), (142, 384), (143, 256), (143, 96)])
 def test_typed_head_matches_oracle_bitwise(smp, ggml_type, d):
-    """Q8_0 and Q4_0 rows of whole blocks take the block dot order, other rows one dot."""
+    """Q8_0 / Q4_0 (PQ2_0 / PTQ1_0) rows of whole blocks take the 32- (128-) weight block dot
+    order, Q1_0 rows of whole blocks its signed blocks, other rows one dot."""
     import torch
 
     rng = np.random.default_rng(ggml_type * 7 + d)
@@ -146,8 +152,12 @@ def test_typed_head_matches_oracle_bitwise(smp, ggml_type, d):
     torch.cuda.synchronize()
     w = O.dequant(ggml_type, src, V * d).reshape(V, d)
     xn = O.rms_norm(x, nw, 1e-6)
-    block = 32 if ggml_type in (8, 2) and d % 32 == 0 else 0
-    want = O.matmul_blocked(w, xn, block)
+    block = 32 if ggml_type in (8, 2) and d % 32 == 0 else 128 if ggml_type in (142, 143) and d % 128 == 0 else 0
+    if ggml_type == 41 and d % 128 == 0:
+        block = 128
+        want = O.matmul_signs(w, xn, 128)
+    else:
+        want = O.matmul_blocked(w, xn, block)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
     if block:  # the order matters at this size: the one-dot order differs somewhere
         assert not np.array_equal(O.matmul_f32(w, xn).view(np.uint32), want.view(np.uint32))
@@ -160,7 +170,9 @@ def test_dequant_rejects_partial_blocks_and_other_types(smp):
     with pytest.raises(bfi_smp.SamplerError):
         smp.dequant(8, src, 31)
     with pytest.raises(bfi_smp.SamplerError):
-        smp.dequant(41, src, 128)  # Q1_0: not taken
+        smp.dequant(6, src, 32)  # Q5_0: not taken
+    with pytest.raises(bfi_smp.SamplerError):
+        smp.dequant(143, src, 64)  # PTQ1_0: half a block
 
 
 def test_typed_fused_step_draws_the_oracles_tokens(smp):

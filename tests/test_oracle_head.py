@@ -186,3 +186,81 @@ def test_dequant_k_quants_place_every_weight():
             want.append(np.float32(np.float32(0.5 * sc[j]) * np.float32(nib + extra)) - np.float32(0.25 * mn[j]))
         got = O.dequant(t, blk, 256)
         assert np.array_equal(got, np.array(want, np.float32)), t
+
+
+def _f16(v):
+    return np.array([v], np.float16).view(np.uint8)
+
+
+def test_dequant_one_bit_and_ternary_reference_kats():
+    # q1_0.rs tests: all clear is -d, all set +d; sign bits LSB first
+    blk = np.concatenate([_f16(0.5), np.zeros(16, np.uint8)])
+    assert (O.dequant(41, blk, 128) == -0.5).all()
+    blk[2:] = 0xFF
+    assert (O.dequant(41, blk, 128) == 0.5).all()
+    blk = np.concatenate([_f16(2.0), np.zeros(16, np.uint8)])
+    blk[2], blk[17] = 0b0000_0101, 0b1000_0000
+    out = O.dequant(41, blk, 128)
+    assert out[0] == 2.0 and out[1] == -2.0 and out[2] == 2.0 and out[126] == -2.0 and out[127] == 2.0
+    # ptq1_0.rs tests: zero digits everywhere are -d
+    blk = np.concatenate([np.zeros(26, np.uint8), _f16(2.0)])
+    assert (O.dequant(143, blk, 128) == -2.0).all()
+
+
+def test_dequant_pq2_0_places_every_code():
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 4, (3, 128))
+    raw = np.zeros((3, 34), np.uint8)
+    for b in range(3):
+        raw[b, 0:2] = _f16(0.25 * (b + 1))
+        for j in range(128):
+            raw[b, 2 + j // 4] |= codes[b, j] << (2 * (j % 4))
+    want = ((codes - 1) * (0.25 * (np.arange(3)[:, None] + 1))).astype(np.float32).reshape(-1)
+    assert np.array_equal(O.dequant(142, raw.reshape(-1), 384), want)
+
+
+def _tq_byte(trits):
+    """The base-3 packing the digit reader inverts: the five digits as a fraction of 243 scaled
+    to a byte, rounded up, so that digit n is the top base-3 digit of byte * 3^n mod 256."""
+    q = 0
+    for t in trits:
+        q = q * 3 + int(t)
+    return (q * 256 + 242) // 243
+
+
+def test_dequant_ptq1_0_places_every_trit():
+    # every 5-digit byte decodes back to its digits
+    for q in range(243):
+        digits = [(q // 3 ** (4 - n)) % 3 for n in range(5)]
+        blk = np.zeros(28, np.uint8)
+        blk[0] = _tq_byte(digits)
+        blk[26:28] = _f16(1.0)
+        out = O.dequant(143, blk, 128)
+        assert [int(out[16 * n]) + 1 for n in range(5)] == digits
+    # the layout: weights 0..79 digit j/16 of qs[j%16], 80..119 digit (j-80)/8 of qs[16+(j-80)%8],
+    # 120..127 digit (j-120)/2 of qh[(j-120)%2] (ptq1_0.rs:15-24)
+    rng = np.random.default_rng(11)
+    t = rng.integers(0, 3, 128)
+    dig = {}
+    for j in range(128):
+        at, n = (j % 16, j // 16) if j < 80 else (16 + (j - 80) % 8, (j - 80) // 8) if j < 120 else (24 + (j - 120) % 2, (j - 120) // 2)
+        dig.setdefault(at, [0] * 5)[n] = t[j]
+    blk = np.zeros(28, np.uint8)
+    for at, ds in dig.items():
+        blk[at] = _tq_byte(ds)
+    blk[26:28] = _f16(0.5)
+    assert np.array_equal(O.dequant(143, blk, 128), ((t - 1) * 0.5).astype(np.float32))
+
+
+def test_signed_block_dot_scales_after_the_sum():
+    d = 3 * 2.0 ** -7  # exact in f16
+    w = np.full((1, 128), d, np.float32)
+    x = np.ones((1, 128), np.float32)
+    x[0, 0] = 2.0 ** 24
+    # the ones vanish into 2^24 before the scale; taken product first they would round up
+    assert O.matmul_signs(w, x)[0, 0] == 2.0 ** 24 * d
+    assert O.matmul_blocked(w, x, 128)[0, 0] > 2.0 ** 24 * d
+    # each block its own scale, signs from the weights, blocks added in order
+    w2 = np.concatenate([np.full(128, 1.0), np.full(128, -2.0)]).astype(np.float32)[None]
+    assert O.matmul_signs(w2, np.ones((1, 256), np.float32))[0, 0] == 128.0 - 256.0
+
